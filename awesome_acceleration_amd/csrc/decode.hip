@@ -1,0 +1,473 @@
+// Paged decode attention (gfx950): one query token per sequence against a
+// paged KV cache -- the attend half of the reference's
+// flash_attn_with_kvcache call (model/model.py:233-240).
+//
+// Work decomposition
+//   grid = (partition, kv_head, sequence), 256 threads (4 wavefronts).
+//   A workgroup owns one KV head of one sequence over a partition of
+//   `part_tokens` consecutive context tokens and serves all G = Hq/Hkv query
+//   heads that share that KV head, so each K/V byte is read from HBM once.
+//   Inside the workgroup every 16-lane DPP row owns one token row at a time:
+//   lane li holds head dims [8*li, 8*li+8) and loads them with one 16-byte
+//   global load (two for fp32), so a wavefront reads 4 token rows (4 x 256 B
+//   in bf16) per load instruction and U=4 rows per DPP row are in flight
+//   before the first use.  The 16 rows of a workgroup walk the partition in
+//   lock step (row slot r takes tokens t0 + r, t0 + r + 16, ...).
+//
+// Softmax
+//   Each DPP row keeps its own online-softmax state (running max m, running
+//   sum l, fp32 accumulator for its 8 dims x G heads; Milakov & Gimelshein
+//   2018), in the log2 domain (scores are pre-multiplied by scale*log2 e and
+//   exponentiated with v_exp_f32).  The 16 row states of a workgroup are
+//   merged at the end (cross-row shuffles inside a wave, LDS across waves).
+//   A sequence whose context spans one partition writes the final output
+//   directly; longer contexts write a normalised partial output and its
+//   log-sum-exp to the workspace, and a second kernel combines the
+//   partitions (the FlashDecoding split-K method).
+//
+// Bytes per launch (the HBM roofline): every context token's K and V row of
+// each KV head is read exactly once, 2 * Hkv * D * elem_bytes per token, plus
+// q and out; the reduction adds 2 * B * Hq * P * (D + 1) * 4 bytes when split.
+
+#include "aac_common.h"
+
+namespace aac {
+
+constexpr int kHeadDim = 128;
+constexpr int kRowLanes = 16;  // lanes per token row: 128 dims / 8 per lane
+
+struct DecodeArgs {
+  const void* q;
+  int64_t q_seq_stride;  // elements
+  const void* k_cache;
+  const void* v_cache;
+  int64_t num_blocks;
+  int32_t block_size;
+  const int32_t* block_tables;
+  int32_t max_blocks;
+  const int32_t* lens;  // context length of sequence b = lens[b] + lens_add
+  int32_t lens_add;
+  int32_t n_seqs;
+  int32_t hq;
+  int32_t hkv;
+  float scale_log2;  // softmax scale * log2(e)
+  void* out;
+  int64_t out_seq_stride;  // elements
+  float* ws_o;             // [B][Hq][P][D] normalised partial outputs
+  float* ws_lse;           // [B][Hq][P]    log2-sum-exp of each partition
+  int32_t n_parts;
+  int32_t part_tokens;
+};
+
+// Raw storage for the 8 elements one lane owns in one token row.
+template <Dt DT> struct Raw8 {
+  static constexpr int kWords = Elem<DT>::kBytes * 8 / 16;  // u32x4 words
+  u32x4 w[kWords];
+  __device__ inline void load(const char* p) {
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) w[i] = *reinterpret_cast<const u32x4*>(p + 16 * i);
+  }
+  __device__ inline void zero() {
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) w[i] = u32x4{0, 0, 0, 0};
+  }
+  __device__ inline void unpack(float* f) const {
+    if constexpr (DT == Dt::FP32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[i] = __uint_as_float(w[0][i]);
+        f[4 + i] = __uint_as_float(w[1][i]);
+      }
+    } else {
+      Elem<DT>::unpack8(w[0], f);
+    }
+  }
+};
+
+__device__ __forceinline__ int context_len(const DecodeArgs& a, int b) {
+  int ctx = a.lens[b] + a.lens_add;
+  const int cap = a.max_blocks * a.block_size;
+  ctx = ctx < 0 ? 0 : ctx;
+  return ctx > cap ? cap : ctx;
+}
+
+__device__ __forceinline__ int parts_of(const DecodeArgs& a, int ctx) {
+  int n = (int)cdiv(ctx, a.part_tokens);
+  return n > a.n_parts ? a.n_parts : n;
+}
+
+template <Dt DT>
+__device__ __forceinline__ void store_out2(void* out, int64_t idx, float x0, float x1) {
+  if constexpr (DT == Dt::FP32) {
+    *reinterpret_cast<float2*>(reinterpret_cast<float*>(out) + idx) = make_float2(x0, x1);
+  } else {
+    *reinterpret_cast<u32*>(reinterpret_cast<u16*>(out) + idx) = Elem<DT>::pack2(x0, x1);
+  }
+}
+
+template <Dt DT, int G, int U>
+__global__ __launch_bounds__(256) void decode_paged_kernel(DecodeArgs a) {
+  constexpr int ES = Elem<DT>::kBytes;
+  const int part = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int ctx = context_len(a, b);
+  const int np = parts_of(a, ctx);
+  const int tid = threadIdx.x;
+
+  if (part >= np) {
+    if (part == 0) {  // empty context: zeros (FA2 convention)
+      for (int i = tid; i < G * (kHeadDim / 2); i += 256) {
+        const int g = i / (kHeadDim / 2), d2 = (i % (kHeadDim / 2)) * 2;
+        store_out2<DT>(a.out, (int64_t)b * a.out_seq_stride + (int64_t)(h * G + g) * kHeadDim + d2,
+                       0.f, 0.f);
+      }
+    }
+    return;
+  }
+  const int t0 = part * a.part_tokens;
+  const int t1 = (part == np - 1) ? ctx : t0 + a.part_tokens;
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, grp = lane >> 4;
+  const int rslot = wave * 4 + grp;  // 0..15
+
+  // q for the G heads of this KV head, pre-scaled into the log2 domain.
+  float qf[G][8];
+  {
+    const char* qb = reinterpret_cast<const char*>(a.q) +
+                     ((int64_t)b * a.q_seq_stride + (int64_t)h * G * kHeadDim + li * 8) * ES;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      Raw8<DT> r;
+      r.load(qb + (int64_t)g * kHeadDim * ES);
+      r.unpack(qf[g]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[g][i] *= a.scale_log2;
+    }
+  }
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -1e30f;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+  }
+
+  const int64_t tok_elems = (int64_t)a.hkv * kHeadDim;  // cache row stride (elements)
+  const char* kbase = reinterpret_cast<const char*>(a.k_cache) + ((int64_t)h * kHeadDim + li * 8) * ES;
+  const char* vbase = reinterpret_cast<const char*>(a.v_cache) + ((int64_t)h * kHeadDim + li * 8) * ES;
+  const int32_t* bt = a.block_tables + (int64_t)b * a.max_blocks;
+
+  for (int tb = t0 + rslot; tb < t1; tb += 16 * U) {
+    Raw8<DT> kr[U], vr[U];
+    bool valid[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = tb + 16 * u;
+      valid[u] = t < t1;
+      if (valid[u]) {
+        int blk = bt[t / a.block_size];
+        if (blk < 0 || blk >= a.num_blocks) blk = 0;
+        const int64_t row = (int64_t)blk * a.block_size + t % a.block_size;
+        kr[u].load(kbase + row * tok_elems * ES);
+        vr[u].load(vbase + row * tok_elems * ES);
+      } else {
+        kr[u].zero();
+        vr[u].zero();
+      }
+    }
+    float s[U][G];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float kf[8];
+      kr[u].unpack(kf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
+        d = row16_sum(d);
+        s[u][g] = valid[u] ? d : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = m[g];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][g]);
+      const float alpha = fast_exp2(m[g] - mx);
+      m[g] = mx;
+      l[g] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+#pragma unroll
+      for (int u = 0; u < U; ++u) s[u][g] = fast_exp2(s[u][g] - mx);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float vf[8];
+      vr[u].unpack(vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        l[g] += s[u][g];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(s[u][g], vf[i], acc[g][i]);
+      }
+    }
+  }
+
+  // Merge the 4 DPP rows of this wave (lanes li, li+16, li+32, li+48 hold the
+  // same dims).
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mx = fmaxf(m[g], __shfl_xor(m[g], 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float f = fast_exp2(m[g] - mx);
+    m[g] = mx;
+    l[g] *= f;
+    l[g] += __shfl_xor(l[g], 16);
+    l[g] += __shfl_xor(l[g], 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float x = acc[g][i] * f;
+      x += __shfl_xor(x, 16);
+      x += __shfl_xor(x, 32);
+      acc[g][i] = x;
+    }
+  }
+
+  __shared__ float sm_m[4][G], sm_l[4][G];
+  __shared__ float sm_acc[4][G][kHeadDim];
+  if (grp == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm_acc[wave][g][li * 8 + i] = acc[g][i];
+      if (li == 0) {
+        sm_m[wave][g] = m[g];
+        sm_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  for (int i = tid; i < G * (kHeadDim / 2); i += 256) {
+    const int g = i / (kHeadDim / 2), d2 = (i % (kHeadDim / 2)) * 2;
+    float mx = sm_m[0][g];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) mx = fmaxf(mx, sm_m[w][g]);
+    float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = fast_exp2(sm_m[w][g] - mx);
+      L += sm_l[w][g] * f;
+      o0 += sm_acc[w][g][d2] * f;
+      o1 += sm_acc[w][g][d2 + 1] * f;
+    }
+    const float inv = 1.f / L;
+    const int hq = h * G + g;
+    if (np == 1) {
+      store_out2<DT>(a.out, (int64_t)b * a.out_seq_stride + (int64_t)hq * kHeadDim + d2, o0 * inv,
+                     o1 * inv);
+    } else {
+      const int64_t slot = ((int64_t)b * a.hq + hq) * a.n_parts + part;
+      *reinterpret_cast<float2*>(a.ws_o + slot * kHeadDim + d2) = make_float2(o0 * inv, o1 * inv);
+      if (d2 == 0) a.ws_lse[slot] = mx + __log2f(L);
+    }
+  }
+}
+
+// Combine the partitions of every (sequence, query head) whose context was
+// split: out = sum_p 2^(lse_p - LSE) o_p with LSE = log2 sum_p 2^lse_p.
+template <Dt DT>
+__global__ __launch_bounds__(64) void decode_reduce_kernel(DecodeArgs a) {
+  const int hq = blockIdx.x, b = blockIdx.y;
+  const int np = parts_of(a, context_len(a, b));
+  if (np <= 1) return;
+  const int lane = threadIdx.x;
+  const int64_t slot0 = ((int64_t)b * a.hq + hq) * a.n_parts;
+  float mx = -INFINITY;
+  for (int p = 0; p < np; ++p) mx = fmaxf(mx, a.ws_lse[slot0 + p]);
+  float W = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int p = 0; p < np; ++p) {
+    const float w = fast_exp2(a.ws_lse[slot0 + p] - mx);
+    const float2 o = *reinterpret_cast<const float2*>(a.ws_o + (slot0 + p) * kHeadDim + 2 * lane);
+    W += w;
+    o0 = fmaf(w, o.x, o0);
+    o1 = fmaf(w, o.y, o1);
+  }
+  const float inv = 1.f / W;
+  store_out2<DT>(a.out, (int64_t)b * a.out_seq_stride + (int64_t)hq * kHeadDim + 2 * lane, o0 * inv,
+                 o1 * inv);
+}
+
+// ------------------------------------------------------------------ planning
+struct DecodePlan {
+  int32_t part_tokens;
+  int32_t n_parts;
+  size_t ws_bytes;
+};
+
+static DecodePlan plan_decode(int32_t n_seqs, int32_t hq, int32_t hkv, int32_t block_size,
+                              int32_t max_blocks, int32_t max_context_len, int32_t part_tokens) {
+  DecodePlan p;
+  int64_t cap = (int64_t)max_blocks * block_size;
+  if (max_context_len > 0 && max_context_len < cap) cap = max_context_len;
+  if (cap < 1) cap = 1;
+  int64_t part = part_tokens;
+  if (part <= 0) {
+    // Aim for >= 8 workgroups per CU (256 CUs) while keeping >= 256 tokens
+    // of work per workgroup.
+    const int64_t items = (int64_t)n_seqs * hkv;
+    part = 512;
+    while (part > 256 && items * cdiv(cap, part) < 2048) part /= 2;
+  }
+  if (part > cap) part = cap;
+  p.part_tokens = (int32_t)part;
+  p.n_parts = (int32_t)cdiv(cap, part);
+  p.ws_bytes = p.n_parts > 1 ? (size_t)n_seqs * hq * p.n_parts * (kHeadDim + 1) * sizeof(float) : 0;
+  return p;
+}
+
+template <Dt DT, int G>
+static void launch_decode_t(const DecodeArgs& a, hipStream_t s) {
+  dim3 grid(a.n_parts, a.hkv, a.n_seqs);
+  hipLaunchKernelGGL((decode_paged_kernel<DT, G, 4>), grid, dim3(256), 0, s, a);
+  if (a.n_parts > 1)
+    hipLaunchKernelGGL((decode_reduce_kernel<DT>), dim3(a.hq, a.n_seqs), dim3(64), 0, s, a);
+}
+
+template <Dt DT>
+static int launch_decode_g(const DecodeArgs& a, int g, hipStream_t s) {
+  switch (g) {
+    case 1: launch_decode_t<DT, 1>(a, s); break;
+    case 2: launch_decode_t<DT, 2>(a, s); break;
+    case 4: launch_decode_t<DT, 4>(a, s); break;
+    case 8: launch_decode_t<DT, 8>(a, s); break;
+    default: return AAC_ERR_UNSUPPORTED;
+  }
+  return AAC_OK;
+}
+
+}  // namespace aac
+
+using namespace aac;
+
+extern "C" size_t aac_decode_workspace_bytes(int32_t n_seqs, int32_t n_q_heads, int32_t n_kv_heads,
+                                             int32_t head_dim, int32_t block_size,
+                                             int32_t max_blocks_per_seq, int32_t max_context_len,
+                                             int32_t partition_tokens) {
+  (void)head_dim;
+  if (n_seqs <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || block_size <= 0 || max_blocks_per_seq <= 0)
+    return 0;
+  return plan_decode(n_seqs, n_q_heads, n_kv_heads, block_size, max_blocks_per_seq, max_context_len,
+                     partition_tokens)
+      .ws_bytes;
+}
+
+static int decode_common(const void* q, int64_t q_seq_stride, const void* k_cache,
+                         const void* v_cache, int64_t num_blocks, int32_t block_size,
+                         const int32_t* block_tables, int32_t max_blocks_per_seq,
+                         const int32_t* lens, int32_t lens_add, int32_t n_seqs,
+                         int32_t max_context_len, int32_t n_q_heads, int32_t n_kv_heads,
+                         int32_t head_dim, float scale, void* out, int64_t out_seq_stride,
+                         void* workspace, size_t workspace_bytes, int32_t partition_tokens,
+                         int32_t dtype, hipStream_t stream) {
+  if (n_seqs < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || num_blocks <= 0 || block_size <= 0 ||
+      max_blocks_per_seq <= 0 || q_seq_stride < 0 || out_seq_stride < 0)
+    return AAC_ERR_INVALID_ARGUMENT;
+  if (head_dim != kHeadDim) return AAC_ERR_UNSUPPORTED;
+  if (n_q_heads % n_kv_heads) return AAC_ERR_SHAPE;
+  if (n_seqs == 0) return AAC_OK;
+  if (!q || !k_cache || !v_cache || !block_tables || !lens || !out) return AAC_ERR_INVALID_ARGUMENT;
+  if (q_seq_stride < (int64_t)n_q_heads * head_dim || out_seq_stride < (int64_t)n_q_heads * head_dim)
+    return AAC_ERR_SHAPE;
+  int es;
+  Dt dt;
+  switch (dtype) {
+    case AAC_DTYPE_BF16: es = 2; dt = Dt::BF16; break;
+    case AAC_DTYPE_FP16: es = 2; dt = Dt::FP16; break;
+    case AAC_DTYPE_FP32: es = 4; dt = Dt::FP32; break;
+    default: return AAC_ERR_UNSUPPORTED;
+  }
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 ||
+      (q_seq_stride * es) % 16 || (uintptr_t)out % 8 || (out_seq_stride * es) % 8)
+    return AAC_ERR_MISALIGNED;
+  const DecodePlan plan = plan_decode(n_seqs, n_q_heads, n_kv_heads, block_size,
+                                      max_blocks_per_seq, max_context_len, partition_tokens);
+  if (plan.ws_bytes) {
+    if (!workspace || workspace_bytes < plan.ws_bytes) return AAC_ERR_WORKSPACE;
+    if ((uintptr_t)workspace % 16) return AAC_ERR_MISALIGNED;
+  }
+  DecodeArgs a = {};
+  a.q = q;
+  a.q_seq_stride = q_seq_stride;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
+  a.block_tables = block_tables;
+  a.max_blocks = max_blocks_per_seq;
+  a.lens = lens;
+  a.lens_add = lens_add;
+  a.n_seqs = n_seqs;
+  a.hq = n_q_heads;
+  a.hkv = n_kv_heads;
+  a.scale_log2 = scale * kLog2e;
+  a.out = out;
+  a.out_seq_stride = out_seq_stride;
+  a.n_parts = plan.n_parts;
+  a.part_tokens = plan.part_tokens;
+  if (plan.ws_bytes) {
+    a.ws_o = reinterpret_cast<float*>(workspace);
+    a.ws_lse = a.ws_o + (size_t)n_seqs * n_q_heads * plan.n_parts * kHeadDim;
+  }
+  const int g = n_q_heads / n_kv_heads;
+  int rc;
+  switch (dt) {
+    case Dt::BF16: rc = launch_decode_g<Dt::BF16>(a, g, stream); break;
+    case Dt::FP16: rc = launch_decode_g<Dt::FP16>(a, g, stream); break;
+    default: rc = launch_decode_g<Dt::FP32>(a, g, stream); break;
+  }
+  if (rc != AAC_OK) return rc;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AAC_OK : (int)e;
+}
+
+extern "C" int aac_decode_paged(const void* q, int64_t q_seq_stride, const void* k_cache,
+                                const void* v_cache, int64_t num_blocks, int32_t block_size,
+                                const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                const int32_t* context_lens, int32_t n_seqs,
+                                int32_t max_context_len, int32_t n_q_heads, int32_t n_kv_heads,
+                                int32_t head_dim, float scale, void* out, int64_t out_seq_stride,
+                                void* workspace, size_t workspace_bytes, int32_t partition_tokens,
+                                int32_t dtype, void* stream) {
+  return decode_common(q, q_seq_stride, k_cache, v_cache, num_blocks, block_size, block_tables,
+                       max_blocks_per_seq, context_lens, 0, n_seqs, max_context_len, n_q_heads,
+                       n_kv_heads, head_dim, scale, out, out_seq_stride, workspace,
+                       workspace_bytes, partition_tokens, dtype, (hipStream_t)stream);
+}
+
+extern "C" int aac_decode_append_paged(const void* q, int64_t q_seq_stride, const void* k,
+                                       const void* v, int64_t k_tok_stride, int64_t v_tok_stride,
+                                       void* k_cache, void* v_cache, int64_t num_blocks,
+                                       int32_t block_size, const int32_t* block_tables,
+                                       int32_t max_blocks_per_seq, const int32_t* cache_seqlens,
+                                       int32_t n_seqs, int32_t max_context_len, int32_t n_q_heads,
+                                       int32_t n_kv_heads, int32_t head_dim, float scale, void* out,
+                                       int64_t out_seq_stride, void* workspace,
+                                       size_t workspace_bytes, int32_t partition_tokens,
+                                       int32_t dtype, void* stream) {
+  if (head_dim != kHeadDim) return AAC_ERR_UNSUPPORTED;
+  const int rc = aac_kv_append_paged(k, v, k_tok_stride, v_tok_stride, k_cache, v_cache, num_blocks,
+                                     block_size, block_tables, max_blocks_per_seq, cache_seqlens,
+                                     n_seqs, n_kv_heads, head_dim, dtype, stream);
+  if (rc != AAC_OK) return rc;
+  return decode_common(q, q_seq_stride, k_cache, v_cache, num_blocks, block_size, block_tables,
+                       max_blocks_per_seq, cache_seqlens, 1, n_seqs, max_context_len, n_q_heads,
+                       n_kv_heads, head_dim, scale, out, out_seq_stride, workspace,
+                       workspace_bytes, partition_tokens, dtype, (hipStream_t)stream);
+}

@@ -1,0 +1,159 @@
+"""Host-side paged-KV bookkeeping: block allocation and per-step metadata.
+
+The reference keeps one contiguous slot of ``max_seq_len`` tokens per
+sequence and hands out slot ids lowest-first from a sorted free list
+(engine/cache_manager.py:5-30, inlined in llm.py:318/354/377/436).  The
+paged cache generalises a slot to a list of fixed-size blocks; the slot
+layout is the special case ``block_size = max_seq_len`` with one block per
+sequence, which ``slot_block_tables`` builds so the reference's caches work
+unchanged.
+
+Metadata produced here mirrors llm.py:127-140 (``cu_seqlens``, positions and
+the flat scatter index, called ``slot_mapping``), generalised to block
+tables, and is shipped to the device with a single host-to-device copy per
+tensor.
+"""
+from __future__ import annotations
+
+import bisect
+import math
+from typing import Iterable, Sequence
+
+import numpy as np
+import torch
+
+__all__ = [
+    "SlotCacheManager",
+    "BlockAllocator",
+    "slot_block_tables",
+    "blocks_needed",
+    "prefill_slot_mapping",
+    "decode_slot_mapping",
+    "build_prefill_metadata",
+    "pad_block_tables",
+]
+
+
+class SlotCacheManager:
+    """Lowest-free-first slot allocator with the reference's interface
+    (engine/cache_manager.py:5-30)."""
+
+    def __init__(self, max_num_seqs: int):
+        self.max_num_seqs = max_num_seqs
+        self.free_slots = list(range(max_num_seqs))
+        self.used_slots: set[int] = set()
+
+    def allocate_slot(self) -> int:
+        if not self.free_slots:
+            raise RuntimeError("No free slots available")
+        slot = self.free_slots.pop(0)
+        self.used_slots.add(slot)
+        return slot
+
+    def free_slot(self, slot: int) -> None:
+        if slot in self.used_slots:
+            self.used_slots.remove(slot)
+            bisect.insort(self.free_slots, slot)
+
+    def reset(self) -> None:
+        self.free_slots = list(range(self.max_num_seqs))
+        self.used_slots.clear()
+
+
+class BlockAllocator:
+    """Fixed-size KV block pool, lowest-free-first like the slot allocator.
+
+    ``allocate(n)`` returns ``n`` block ids or raises ``RuntimeError`` when
+    the pool cannot supply them (the pool is left unchanged).  ``free``
+    returns ids to the pool; freeing an id that is not allocated is ignored,
+    as ``SlotCacheManager.free_slot`` ignores unknown slots.
+    """
+
+    def __init__(self, num_blocks: int):
+        if num_blocks <= 0:
+            raise ValueError("num_blocks must be positive")
+        self.num_blocks = num_blocks
+        self._free = list(range(num_blocks))
+        self._used: set[int] = set()
+
+    @property
+    def num_free(self) -> int:
+        return len(self._free)
+
+    def allocate(self, n: int) -> list[int]:
+        if n < 0:
+            raise ValueError("n must be >= 0")
+        if n > len(self._free):
+            raise RuntimeError(f"No free blocks available (need {n}, have {len(self._free)})")
+        out, self._free = self._free[:n], self._free[n:]
+        self._used.update(out)
+        return out
+
+    def free(self, blocks: Iterable[int]) -> None:
+        for b in blocks:
+            if b in self._used:
+                self._used.remove(b)
+                bisect.insort(self._free, b)
+
+    def reset(self) -> None:
+        self._free = list(range(self.num_blocks))
+        self._used.clear()
+
+
+def blocks_needed(n_tokens: int, block_size: int) -> int:
+    return max(0, math.ceil(n_tokens / block_size))
+
+
+def slot_block_tables(slot_indices: Sequence[int]) -> np.ndarray:
+    """Block tables of the reference's slot layout: one block (= slot) per sequence."""
+    return np.asarray(slot_indices, dtype=np.int32).reshape(-1, 1)
+
+
+def pad_block_tables(tables: Sequence[Sequence[int]], width: int | None = None,
+                     fill: int = 0) -> np.ndarray:
+    """Rectangular int32 ``[B, width]`` array from ragged block lists."""
+    width = width if width is not None else max((len(t) for t in tables), default=1)
+    out = np.full((len(tables), max(width, 1)), fill, dtype=np.int32)
+    for i, t in enumerate(tables):
+        if len(t) > width:
+            raise ValueError("block list longer than the table width")
+        out[i, :len(t)] = t
+    return out
+
+
+def prefill_slot_mapping(block_tables: np.ndarray, seq_lens: Sequence[int], block_size: int,
+                         start_positions: Sequence[int] | None = None) -> np.ndarray:
+    """Flat cache row of every packed prefill token (paged form of llm.py:139-140)."""
+    bt = np.asarray(block_tables, dtype=np.int64)
+    parts = []
+    for b, L in enumerate(seq_lens):
+        p0 = 0 if start_positions is None else int(start_positions[b])
+        p = np.arange(p0, p0 + int(L), dtype=np.int64)
+        parts.append(bt[b, p // block_size] * block_size + p % block_size)
+    return np.concatenate(parts) if parts else np.zeros(0, dtype=np.int64)
+
+
+def decode_slot_mapping(block_tables: np.ndarray, positions: Sequence[int],
+                        block_size: int) -> np.ndarray:
+    """Flat cache row of the token each decode sequence appends at ``positions[b]``."""
+    bt = np.asarray(block_tables, dtype=np.int64)
+    p = np.asarray(positions, dtype=np.int64)
+    return bt[np.arange(p.shape[0]), p // block_size] * block_size + p % block_size
+
+
+def build_prefill_metadata(seq_lens: Sequence[int], block_tables: np.ndarray, block_size: int,
+                           device: torch.device | str):
+    """``(cu_seqlens int32 [n+1], positions int64 [N], slot_mapping int64 [N])`` on ``device``.
+
+    Same values as llm.py:129-140 for the slot layout; each tensor is built on
+    the host and copied once (the reference issues one small copy per list
+    and a device-side ``repeat_interleave``).
+    """
+    lens = np.asarray(seq_lens, dtype=np.int64)
+    cu = np.zeros(lens.shape[0] + 1, dtype=np.int32)
+    np.cumsum(lens, out=cu[1:])
+    positions = (np.concatenate([np.arange(L, dtype=np.int64) for L in lens])
+                 if lens.size else np.zeros(0, dtype=np.int64))
+    slots = prefill_slot_mapping(block_tables, lens, block_size)
+    to = lambda a: torch.from_numpy(a).to(device, non_blocking=False)  # noqa: E731
+    return to(cu), to(positions), to(slots)

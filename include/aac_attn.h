@@ -1,0 +1,198 @@
+/*
+ * aac_attn.h -- C ABI of libaac_attn.so, the MI355X (gfx950) attention hot
+ * path of the Qwen3 serving engine: the slot_mapping KV-cache store, varlen
+ * causal GQA prefill and paged decode.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor pointers are device pointers; every buffer is owned by the
+ *     caller.  The library allocates no device memory.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Work is enqueued asynchronously; no entry point synchronises the host.
+ *   - Strides are in ELEMENTS.  Within one token the [heads, head_dim] block
+ *     must be contiguous (head stride == head_dim, dim stride == 1); only the
+ *     token (or sequence) stride is free.  This admits the reference's v,
+ *     a strided view of the fused qkv buffer with token stride
+ *     (Hq + 2*Hkv) * head_dim (llm.py:156, model/model.py:222).
+ *   - Caches are [num_blocks, block_size, n_kv_heads, head_dim], token-major
+ *     ("NHD").  The reference's slot cache [num_slots, max_seq_len, Hkv, D]
+ *     (model/model.py:324-336) is the case block_size = max_seq_len with one
+ *     block per sequence (block_tables[b] = {slot_b}).
+ *   - Return value: 0 on success, a negative AAC_ERR_* code for a rejected
+ *     argument, or a positive hipError_t when a launch failed.  Nothing is
+ *     thrown across the ABI; aac_strerror() gives the message.
+ *   - Calls are stateless and reentrant.
+ *
+ * Reference interfaces replaced (reference paths are relative to the
+ * yijichar/AWesome_ACceleration tree):
+ *   aac_kv_store             kv_flat.index_copy_(0, scatter_indices, k)/(v)
+ *                            llm.py:171-174
+ *   aac_kv_append_paged      the k=/v= append half of flash_attn_with_kvcache
+ *                            model/model.py:233-240
+ *   aac_prefill_varlen       flash_attn_varlen_func(..., causal=True)
+ *                            llm.py:178-184 (also flash_attn_func,
+ *                            model/model.py:253-254, with uniform cu_seqlens)
+ *   aac_prefill_varlen_store llm.py:171-184 (store + attend in one call)
+ *   aac_decode_paged         the attend half of flash_attn_with_kvcache
+ *                            model/model.py:233-240
+ *   aac_decode_append_paged  all of flash_attn_with_kvcache(k=, v=)
+ *                            model/model.py:233-240
+ */
+#ifndef AAC_ATTN_H
+#define AAC_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AAC_ABI_VERSION 1
+
+/* element types */
+enum {
+  AAC_DTYPE_BF16 = 0,
+  AAC_DTYPE_FP16 = 1,
+  AAC_DTYPE_FP32 = 2
+};
+
+/* status codes (positive values are hipError_t) */
+enum {
+  AAC_OK = 0,
+  AAC_ERR_INVALID_ARGUMENT = -1, /* null pointer, negative or zero size  */
+  AAC_ERR_UNSUPPORTED = -2,      /* dtype / head_dim / GQA group not built */
+  AAC_ERR_MISALIGNED = -3,       /* pointer or stride breaks 16-B access  */
+  AAC_ERR_WORKSPACE = -4,        /* split-K workspace too small           */
+  AAC_ERR_SHAPE = -5             /* inconsistent shape arguments          */
+};
+
+/* ABI revision of the loaded library (AAC_ABI_VERSION it was built with). */
+int aac_abi_version(void);
+
+/* Message for a status code returned by any entry point (never NULL). */
+const char* aac_strerror(int code);
+
+/*
+ * KV store: for t in [0, n_tokens):
+ *   if slot_mapping[t] >= 0:
+ *     k_cache_rows[slot_mapping[t]] = k[t];  v_cache_rows[slot_mapping[t]] = v[t]
+ * where *_cache_rows views the cache as [num_cache_rows, n_kv_heads, head_dim].
+ * Byte copy: the cache contents are bit-exact.  A negative slot is padding and
+ * is skipped; a slot >= num_cache_rows is skipped too (never written), which the
+ * reference would reject with an IndexError -- validate on the host if that
+ * matters.  Duplicate slots leave an unspecified one of the rows.
+ * Replaces llm.py:171-174.
+ */
+int aac_kv_store(const void* k, const void* v, int64_t k_tok_stride, int64_t v_tok_stride,
+                 void* k_cache, void* v_cache, int64_t num_cache_rows,
+                 const int64_t* slot_mapping, int64_t n_tokens, int32_t n_kv_heads,
+                 int32_t head_dim, int32_t dtype, void* stream);
+
+/*
+ * Decode append: the new token of sequence b (k[b], v[b]) is written at
+ * position p = cache_seqlens[b], i.e. cache row
+ *   block_tables[b * max_blocks_per_seq + p / block_size] * block_size + p % block_size.
+ * cache_seqlens is NOT modified (the reference's caller increments it,
+ * model/model.py:241).  Positions beyond the table capacity and block ids
+ * outside [0, num_blocks) are skipped.
+ * Replaces the k=/v= half of flash_attn_with_kvcache (model/model.py:233-240).
+ */
+int aac_kv_append_paged(const void* k, const void* v, int64_t k_tok_stride, int64_t v_tok_stride,
+                        void* k_cache, void* v_cache, int64_t num_blocks, int32_t block_size,
+                        const int32_t* block_tables, int32_t max_blocks_per_seq,
+                        const int32_t* cache_seqlens, int32_t n_seqs, int32_t n_kv_heads,
+                        int32_t head_dim, int32_t dtype, void* stream);
+
+/*
+ * Varlen attention over packed segments.  Segment s owns query rows
+ * [cu_seqlens_q[s], cu_seqlens_q[s+1]) and key rows
+ * [cu_seqlens_k[s], cu_seqlens_k[s+1]).  Query head h reads KV head
+ * h / (n_q_heads / n_kv_heads).  With causal != 0 the mask is bottom-right
+ * aligned (query i sees keys j <= i + Lk - Lq); a query row that sees no key
+ * gets zeros.  Softmax in fp32, output rounded to dtype.
+ *   q   [Nq, n_q_heads, head_dim]  token stride q_tok_stride
+ *   k,v [Nk, n_kv_heads, head_dim] token strides k_tok_stride / v_tok_stride
+ *   out [Nq, n_q_heads, head_dim]  token stride out_tok_stride
+ * max_seqlen_q / max_seqlen_k bound the segment lengths (as in FA2; they size
+ * the launch grid).  Built for dtype BF16/FP16, head_dim 128, group 1/2/4/8.
+ * Replaces flash_attn_varlen_func (llm.py:178-184).
+ */
+int aac_prefill_varlen(const void* q, const void* k, const void* v, int64_t q_tok_stride,
+                       int64_t k_tok_stride, int64_t v_tok_stride, const int32_t* cu_seqlens_q,
+                       const int32_t* cu_seqlens_k, int32_t n_seqs, int32_t max_seqlen_q,
+                       int32_t max_seqlen_k, int32_t n_q_heads, int32_t n_kv_heads,
+                       int32_t head_dim, float scale, int32_t causal, void* out,
+                       int64_t out_tok_stride, int32_t dtype, void* stream);
+
+/*
+ * aac_kv_store(k, v -> caches via slot_mapping) followed by
+ * aac_prefill_varlen on the same stream: the whole per-layer attention block
+ * of the reference's prefill (llm.py:171-184).  slot_mapping has Nk entries.
+ */
+int aac_prefill_varlen_store(const void* q, const void* k, const void* v, int64_t q_tok_stride,
+                             int64_t k_tok_stride, int64_t v_tok_stride,
+                             const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                             int32_t n_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                             int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                             int32_t causal, void* out, int64_t out_tok_stride, void* k_cache,
+                             void* v_cache, int64_t num_cache_rows, const int64_t* slot_mapping,
+                             int32_t dtype, void* stream);
+
+/*
+ * Bytes of split-K workspace aac_decode_paged needs for this shape.
+ * max_context_len <= 0 means "table capacity" (max_blocks_per_seq *
+ * block_size), partition_tokens <= 0 means "library's choice".  Returns 0
+ * when the chosen plan needs no workspace.
+ */
+size_t aac_decode_workspace_bytes(int32_t n_seqs, int32_t n_q_heads, int32_t n_kv_heads,
+                                  int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
+                                  int32_t max_context_len, int32_t partition_tokens);
+
+/*
+ * Paged decode attention: one query token per sequence,
+ *   out[b, h] = softmax(scale * q[b, h] . K_b^T) V_b
+ * over the first context_lens[b] tokens of sequence b, located through
+ * block_tables[b * max_blocks_per_seq + i] (physical block of tokens
+ * [i*block_size, (i+1)*block_size)).  context_lens[b] == 0 gives zeros; a
+ * context longer than the table capacity is clamped to it.  Block ids outside
+ * [0, num_blocks) are read as block 0 (output undefined, memory safe).
+ *   q   [n_seqs, n_q_heads, head_dim]  seq stride q_seq_stride
+ *   out [n_seqs, n_q_heads, head_dim]  seq stride out_seq_stride
+ * Long contexts are split into partitions of partition_tokens (<= 0: auto)
+ * that are combined with a log-sum-exp reduction in `workspace`
+ * (aac_decode_workspace_bytes).  max_context_len (<= 0: table capacity) is
+ * an upper bound on context_lens used to size the grid.
+ * Built for dtype BF16/FP16/FP32, head_dim 128, group 1/2/4/8.
+ * Replaces the attend half of flash_attn_with_kvcache (model/model.py:233-240).
+ */
+int aac_decode_paged(const void* q, int64_t q_seq_stride, const void* k_cache, const void* v_cache,
+                     int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
+                     int32_t max_blocks_per_seq, const int32_t* context_lens, int32_t n_seqs,
+                     int32_t max_context_len, int32_t n_q_heads, int32_t n_kv_heads,
+                     int32_t head_dim, float scale, void* out, int64_t out_seq_stride,
+                     void* workspace, size_t workspace_bytes, int32_t partition_tokens,
+                     int32_t dtype, void* stream);
+
+/*
+ * flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v, cache_seqlens,
+ * block_table, softmax_scale, causal=False): append k/v at position
+ * cache_seqlens[b] (aac_kv_append_paged), then attend over
+ * cache_seqlens[b] + 1 tokens.  cache_seqlens is not modified.
+ * max_context_len bounds cache_seqlens[b] + 1 (<= 0: table capacity).
+ * Replaces model/model.py:233-240.
+ */
+int aac_decode_append_paged(const void* q, int64_t q_seq_stride, const void* k, const void* v,
+                            int64_t k_tok_stride, int64_t v_tok_stride, void* k_cache,
+                            void* v_cache, int64_t num_blocks, int32_t block_size,
+                            const int32_t* block_tables, int32_t max_blocks_per_seq,
+                            const int32_t* cache_seqlens, int32_t n_seqs, int32_t max_context_len,
+                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                            void* out, int64_t out_seq_stride, void* workspace,
+                            size_t workspace_bytes, int32_t partition_tokens, int32_t dtype,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AAC_ATTN_H */

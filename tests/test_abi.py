@@ -1,0 +1,69 @@
+"""The C-ABI library loads, exports every symbol include/aac_attn.h declares,
+and rejects bad arguments on the host (no GPU work is issued here)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from awesome_acceleration_amd import _lib
+from awesome_acceleration_amd.build import LIB_PATH
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "aac_attn.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(aac_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    assert LIB_PATH.exists(), "build the library first (__graft_entry__.build())"
+    handle = ctypes.CDLL(str(LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(handle, name), name
+
+
+def test_abi_version_and_messages():
+    L = _lib.lib()
+    assert L.aac_abi_version() == _lib.ABI_VERSION
+    for code in (0, -1, -2, -3, -4, -5):
+        assert L.aac_strerror(code)
+    assert b"unknown" in L.aac_strerror(-99)
+
+
+def test_host_side_argument_rejection():
+    L = _lib.lib()
+    # null pointers with work to do -> AAC_ERR_INVALID_ARGUMENT, before any launch
+    assert L.aac_kv_store(None, None, 1024, 1024, None, None, 16, None, 4, 8, 128, 0, None) == -1
+    # zero tokens is a no-op success
+    assert L.aac_kv_store(None, None, 1024, 1024, None, None, 16, None, 0, 8, 128, 0, None) == 0
+    # unknown dtype
+    assert L.aac_kv_store(None, None, 1024, 1024, None, None, 16, None, 4, 8, 128, 9, None) == -2
+    # head_dim other than 128 is not built for decode
+    assert L.aac_decode_paged(None, 0, None, None, 1, 16, None, 1, None, 1, 0, 4, 2, 64, 1.0,
+                              None, 0, None, 0, 0, 0, None) == -2
+    # Hq not a multiple of Hkv
+    assert L.aac_decode_paged(None, 0, None, None, 1, 16, None, 1, None, 1, 0, 6, 4, 128, 1.0,
+                              None, 0, None, 0, 0, 0, None) == -5
+    # prefill: fp32 is not supported on the MFMA path
+    assert L.aac_prefill_varlen(None, None, None, 0, 0, 0, None, None, 1, 1, 1, 16, 8, 128,
+                                1.0, 1, None, 0, 2, None) == -2
+
+
+def test_workspace_sizing():
+    L = _lib.lib()
+    # context that fits one partition needs no workspace
+    assert L.aac_decode_workspace_bytes(4, 16, 8, 128, 256, 1, 0, 256) == 0
+    # 8 blocks of 256 split in 512-token partitions: 4 partitions x (128 + 1) floats
+    n = L.aac_decode_workspace_bytes(256, 16, 8, 128, 256, 8, 0, 512)
+    assert n == 256 * 16 * 4 * 129 * 4
+
+
+def test_check_raises_runtime_error():
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.check(-1, "probe")

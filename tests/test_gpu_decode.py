@@ -1,0 +1,229 @@
+"""GPU parity of paged decode (store then attend) against the oracle.
+
+Covers the committed fixtures (fp32 Qwen3-0.6B layer at batch 4, tiny bf16),
+the 256-sequence bf16 decode at full size, the long-context GQA-4 decode
+(B=64, 16k-32k tokens) on a sample of sequences, the reference's slot layout
+through flash_attn_with_kvcache(cache_batch_idx=...), every GQA group, and
+the invariants of the split-K plan (partition count, block relabelling).
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from awesome_acceleration_amd import flash_attn_interface as fai
+from cases import config1_inputs, sha256, tiny_decode_inputs
+from gpu_util import bf16_np_to_f64, bytes_of, check_attention, f64, np_of, t_of
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+MANIFEST = json.loads((GOLD / "manifest.json").read_text())
+
+
+def _run_fixture(inp, gpu, dtype):
+    q = t_of(inp["q"], gpu, dtype)
+    kc = t_of(inp["k_cache"], gpu, dtype)
+    vc = t_of(inp["v_cache"], gpu, dtype)
+    kn = t_of(inp["k_new"], gpu, dtype)
+    vn = t_of(inp["v_new"], gpu, dtype)
+    bt = torch.from_numpy(inp["block_tables"]).to(gpu)
+    lens = torch.from_numpy(inp["cache_seqlens"]).to(gpu)
+    B, hq, d = q.shape
+    out = fai.flash_attn_with_kvcache(q.view(B, 1, hq, d), kc, vc, k=kn.view(B, 1, -1, d),
+                                      v=vn.view(B, 1, -1, d), cache_seqlens=lens, block_table=bt,
+                                      softmax_scale=inp["scale"], causal=False)
+    torch.cuda.synchronize()
+    return out.view(B, hq, d), kc, vc, lens
+
+
+def test_config1_fp32_fixture(gpu):
+    print("case: config1 fp32 decode fixture", flush=True)
+    inp = config1_inputs()
+    fx = np.load(GOLD / "config1_decode_fp32.npz")
+    out, kc, vc, lens = _run_fixture(inp, gpu, torch.float32)
+    man = MANIFEST["config1_decode_fp32"]
+    assert sha256(np_of(kc)) == man["digest_k_cache_after"]
+    assert sha256(np_of(vc)) == man["digest_v_cache_after"]
+    assert np.array_equal(np_of(lens), inp["cache_seqlens"])  # not modified
+    check_attention(out, fx["out"], atol=1e-4, what="config1 fp32")
+
+
+def test_tiny_bf16_fixture(gpu):
+    print("case: tiny bf16 decode fixture", flush=True)
+    inp = tiny_decode_inputs()
+    fx = np.load(GOLD / "tiny_decode_bf16.npz")
+    out, kc, vc, _ = _run_fixture(inp, gpu, None)
+    man = MANIFEST["tiny_decode_bf16"]
+    assert sha256(np_of(kc)) == man["digest_k_cache_after"]
+    assert sha256(np_of(vc)) == man["digest_v_cache_after"]
+    check_attention(out, fx["out"], what="tiny bf16")
+
+
+def _random_paged(B, hq, hkv, ctx, bs, seed, gpu, dtype=torch.bfloat16, extra_blocks=3):
+    """Shared shuffled pool holding exactly the blocks the sequences need."""
+    rs = np.random.RandomState(seed)
+    need = [int(np.ceil(c / bs)) for c in ctx]
+    pool = sum(need) + extra_blocks
+    perm = rs.permutation(pool).astype(np.int32)
+    width = max(need)
+    bt = np.zeros((B, width), np.int32)
+    k0 = 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[k0:k0 + n]
+        k0 += n
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    kc = torch.randn((pool, bs, hkv, 128), generator=g, device=gpu, dtype=torch.float32).to(dtype)
+    vc = torch.randn((pool, bs, hkv, 128), generator=g, device=gpu, dtype=torch.float32).to(dtype)
+    q = torch.randn((B, hq, 128), generator=g, device=gpu, dtype=torch.float32).to(dtype)
+    kn = torch.randn((B, hkv, 128), generator=g, device=gpu, dtype=torch.float32).to(dtype)
+    vn = torch.randn((B, hkv, 128), generator=g, device=gpu, dtype=torch.float32).to(dtype)
+    return q, kc, vc, kn, vn, bt
+
+
+def _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, seqs, scale):
+    out = {}
+    for b in seqs:
+        ks = oracle.gather_paged(kc_np, bt[b], int(ctx[b]), bs)
+        vs = oracle.gather_paged(vc_np, bt[b], int(ctx[b]), bs)
+        if ks.dtype == np.uint16:
+            ks, vs, qb = bf16_np_to_f64(ks), bf16_np_to_f64(vs), bf16_np_to_f64(q_np[b])
+        else:
+            ks, vs, qb = ks.astype(np.float64), vs.astype(np.float64), q_np[b].astype(np.float64)
+        out[b] = oracle.paged_decode(qb[None], ks[None], vs[None],
+                                     np.arange(1, dtype=np.int32)[None], [int(ctx[b])],
+                                     block_size=int(ctx[b]), scale=scale)[0]
+    return out
+
+
+def test_decode_256_seqs_full_size(gpu):
+    # bf16, 256 sequences, 16/8 heads, D=128, context ~ U[1024, 2047] (after
+    # the store), block 256, shuffled shared pool; store one token, attend.
+    print("case: decode 256 seqs full size", flush=True)
+    B, hq, hkv, bs = 256, 16, 8, 256
+    rs = np.random.RandomState(0)
+    ctx = rs.randint(1024, 2048, B).astype(np.int32)
+    q, kc, vc, kn, vn, bt = _random_paged(B, hq, hkv, ctx, bs, 0, gpu)
+    scale = 128 ** -0.5
+    lens = torch.from_numpy(ctx - 1).to(gpu)
+    bt_g = torch.from_numpy(bt).to(gpu)
+    out = fai.flash_attn_with_kvcache(q.view(B, 1, hq, 128), kc, vc, k=kn.view(B, 1, hkv, 128),
+                                      v=vn.view(B, 1, hkv, 128), cache_seqlens=lens,
+                                      block_table=bt_g, softmax_scale=scale)
+    torch.cuda.synchronize()
+    kc_np, vc_np, q_np = np_of(kc), np_of(vc), np_of(q)
+    # the appended rows are in the cache now (bit-exact store)
+    sm = oracle.decode_slot_mapping(bt, ctx - 1, bs)
+    assert np.array_equal(kc_np.reshape(-1, hkv, 128)[sm], np_of(kn))
+    assert np.array_equal(vc_np.reshape(-1, hkv, 128)[sm], np_of(vn))
+    ref = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), scale)
+    check_attention(out.view(B, hq, 128), np.stack([ref[b] for b in range(B)]),
+                    what="decode 256 seqs")
+
+
+def test_decode_long_context_gqa4_sampled(gpu):
+    # bf16, B=64, 32 query / 8 KV heads, context ~ U[16384, 32768]: split-K
+    # with the log-sum-exp reduction.  8 sequences are checked against the
+    # oracle; all 64 against the same kernel under other partition sizes.
+    print("case: decode long context gqa4", flush=True)
+    B, hq, hkv, bs = 64, 32, 8, 256
+    rs = np.random.RandomState(1)
+    ctx = rs.randint(16384, 32769, B).astype(np.int32)
+    q, kc, vc, _, _, bt = _random_paged(B, hq, hkv, ctx, bs, 1, gpu, extra_blocks=0)
+    scale = 128 ** -0.5
+    bt_g = torch.from_numpy(bt).to(gpu)
+    ctx_g = torch.from_numpy(ctx).to(gpu)
+    out = fai.decode_paged(q, kc, vc, bt_g, ctx_g, scale, max_context_len=32768)
+    alt = [fai.decode_paged(q, kc, vc, bt_g, ctx_g, scale, partition_tokens=p)
+           for p in (1024, 4096)]
+    torch.cuda.synchronize()
+    for a in alt:  # partitioning changes only fp32 summation order
+        assert float((a.float() - out.float()).abs().max()) <= 2 ** -8
+    sample = [0, 7, 19, 33, 40, 51, 60, 63]
+    q_np = np_of(q)
+    bt_s = bt[sample]
+    used = np.unique(bt_s)
+    # copy only the sampled sequences' blocks to the host
+    remap = {int(b): i for i, b in enumerate(used)}
+    kc_np = np_of(kc[torch.from_numpy(used.astype(np.int64)).to(gpu)])
+    vc_np = np_of(vc[torch.from_numpy(used.astype(np.int64)).to(gpu)])
+    bt_local = np.vectorize(lambda x: remap[int(x)])(bt_s).astype(np.int32)
+    for i, b in enumerate(sample):
+        ref = _oracle_rows(kc_np, vc_np, q_np[b:b + 1], bt_local[i:i + 1], ctx[b:b + 1], bs, [0],
+                           scale)[0]
+        check_attention(out[b], ref, what=f"long ctx seq {b}")
+
+
+def test_reference_slot_layout_via_cache_batch_idx(gpu):
+    # The reference's cache [num_slots, max_seq_len, Hkv, D] with
+    # cache_batch_idx picking the slot (model/model.py:233-240); max_seq_len
+    # 2064 is not a power of two.
+    print("case: slot layout", flush=True)
+    S, lmax, B, hq, hkv = 12, 2064, 5, 16, 8
+    g = torch.Generator(device=gpu).manual_seed(4)
+    kc = torch.randn((S, lmax, hkv, 128), generator=g, device=gpu).to(torch.bfloat16)
+    vc = torch.randn((S, lmax, hkv, 128), generator=g, device=gpu).to(torch.bfloat16)
+    q = torch.randn((B, 1, hq, 128), generator=g, device=gpu).to(torch.bfloat16)
+    # k/v as strided views of a fused qkv buffer, like model/model.py:221-222
+    qkv = torch.randn((B, 1, (hq + 2 * hkv) * 128), generator=g, device=gpu).to(torch.bfloat16)
+    k = qkv[..., hq * 128:(hq + hkv) * 128].view(B, 1, hkv, 128)
+    v = qkv[..., (hq + hkv) * 128:].view(B, 1, hkv, 128)
+    slots = torch.tensor([7, 0, 11, 3, 5], dtype=torch.int64, device=gpu)
+    seqlens = torch.tensor([0, 1000, 2063, 17, 255], dtype=torch.int32, device=gpu)
+    kc_before = np_of(kc)
+    vc_before = np_of(vc)
+    out = fai.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=seqlens,
+                                      cache_batch_idx=slots.int(), softmax_scale=128 ** -0.5)
+    torch.cuda.synchronize()
+    # oracle: store then attend, slot layout
+    bt = slots.cpu().numpy().astype(np.int32).reshape(B, 1)
+    ref, new_lens = oracle.decode_append_attend(
+        np_of(q).reshape(B, hq, 128), kc_before, vc_before, np_of(k.contiguous()).reshape(B, hkv, 128),
+        np_of(v.contiguous()).reshape(B, hkv, 128), bt, seqlens.cpu().numpy(), lmax, 128 ** -0.5)
+    assert np.array_equal(np_of(kc), kc_before)  # oracle stored into kc_before in place
+    assert np.array_equal(np_of(vc), vc_before)
+    check_attention(out.view(B, hq, 128), ref, what="slot layout")
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_gqa_groups_and_dtypes(gpu, hq, hkv, dtype):
+    print(f"case: gqa {hq}/{hkv} {dtype}", flush=True)
+    B, bs = 6, 32
+    ctx = np.array([1, 31, 32, 33, 300, 777], np.int32)
+    q, kc, vc, _, _, bt = _random_paged(B, hq, hkv, ctx, bs, 5, gpu, dtype)
+    bt_g, ctx_g = torch.from_numpy(bt).to(gpu), torch.from_numpy(ctx).to(gpu)
+    for part in (0, 64, 100):
+        out = fai.decode_paged(q, kc, vc, bt_g, ctx_g, 0.1, partition_tokens=part)
+        torch.cuda.synchronize()
+        kc_np, vc_np = f64(kc), f64(vc)
+        q_np = f64(q)
+        ref = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), 0.1)
+        check_attention(out, np.stack([ref[b] for b in range(B)]), what=f"gqa part={part}")
+
+
+def test_decode_edge_cases_and_block_relabelling(gpu):
+    print("case: decode edges", flush=True)
+    B, hq, hkv, bs = 4, 16, 8, 64
+    ctx = np.array([0, 1, 64, 513], np.int32)
+    q, kc, vc, _, _, bt = _random_paged(B, hq, hkv, np.maximum(ctx, 1), bs, 6, gpu)
+    bt_g, ctx_g = torch.from_numpy(bt).to(gpu), torch.from_numpy(ctx).to(gpu)
+    out = fai.decode_paged(q, kc, vc, bt_g, ctx_g, 128 ** -0.5, partition_tokens=128)
+    torch.cuda.synchronize()
+    assert not out[0].any()  # empty context -> zeros
+    v0 = vc[bt[1, 0], 0]  # [hkv, D]; context 1 returns v0 of the KV head
+    assert torch.equal(out[1], v0.repeat_interleave(hq // hkv, 0))
+    # relabel the physical blocks: identical bits
+    pool = kc.shape[0]
+    perm = torch.randperm(pool, generator=torch.Generator().manual_seed(7))
+    kc2 = torch.empty_like(kc)
+    vc2 = torch.empty_like(vc)
+    kc2[perm.to(gpu)] = kc
+    vc2[perm.to(gpu)] = vc
+    bt2 = perm.numpy()[bt].astype(np.int32)
+    out2 = fai.decode_paged(q, kc2, vc2, torch.from_numpy(bt2).to(gpu), ctx_g, 128 ** -0.5,
+                            partition_tokens=128)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
