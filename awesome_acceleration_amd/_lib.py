@@ -41,7 +41,7 @@ SIGNATURES: dict[str, tuple] = {
     "aac_prefill_varlen_store": (
         _c_int,
         [_p, _p, _p, _i64, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
-         _p, _i64, _p, _p, _i64, _p, _i32, _p],
+         _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p],
     ),
     "aac_decode_workspace_bytes": (_size, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "aac_decode_paged": (

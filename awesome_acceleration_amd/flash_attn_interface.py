@@ -209,7 +209,7 @@ def varlen_prefill_with_kvcache(q, k, v, cu_seqlens, max_seqlen, k_cache, v_cach
         cu_seqlens.data_ptr(), cu_seqlens.shape[0] - 1, int(max_seqlen), int(max_seqlen),
         q.shape[1], k.shape[1], q.shape[2], scale, int(bool(causal)), out.data_ptr(),
         out.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), rows, slot_mapping.data_ptr(),
-        _dtype_code(q), _stream(q))
+        k.shape[0], _dtype_code(q), _stream(q))
     _lib.check(rc, "aac_prefill_varlen_store")
     return out
 

@@ -127,7 +127,8 @@ int aac_prefill_varlen(const void* q, const void* k, const void* v, int64_t q_to
 /*
  * aac_kv_store(k, v -> caches via slot_mapping) followed by
  * aac_prefill_varlen on the same stream: the whole per-layer attention block
- * of the reference's prefill (llm.py:171-184).  slot_mapping has Nk entries.
+ * of the reference's prefill (llm.py:171-184).  slot_mapping has n_kv_tokens
+ * entries, one per packed key token (n_kv_tokens = cu_seqlens_k[n_seqs]).
  */
 int aac_prefill_varlen_store(const void* q, const void* k, const void* v, int64_t q_tok_stride,
                              int64_t k_tok_stride, int64_t v_tok_stride,
@@ -136,7 +137,7 @@ int aac_prefill_varlen_store(const void* q, const void* k, const void* v, int64_
                              int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
                              int32_t causal, void* out, int64_t out_tok_stride, void* k_cache,
                              void* v_cache, int64_t num_cache_rows, const int64_t* slot_mapping,
-                             int32_t dtype, void* stream);
+                             int64_t n_kv_tokens, int32_t dtype, void* stream);
 
 /*
  * Bytes of split-K workspace aac_decode_paged needs for this shape.

@@ -1,0 +1,144 @@
+"""GPU parity of the varlen prefill kernel (and the store in the same call)
+against the oracle: committed fixture, the 8 x 1024 Qwen3-0.6B layer at full
+size, ragged/empty segments, every GQA group, fp16, non-causal, Lq != Lk,
+and the padded flash_attn_func surface."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from awesome_acceleration_amd import flash_attn_interface as fai, paged
+from gpu_util import bytes_of, check_attention, f64, np_of, t_of
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def test_tiny_prefill_fixture(gpu):
+    print("case: tiny prefill fixture", flush=True)
+    fx = np.load(GOLD / "tiny_prefill_bf16.npz")
+    q, k, v = (t_of(fx[n], gpu) for n in ("q", "k", "v"))
+    cu = torch.from_numpy(fx["cu_seqlens"]).to(gpu)
+    L = int(np.diff(fx["cu_seqlens"]).max())
+    out = fai.flash_attn_varlen_func(q, k, v, cu, cu, L, L, softmax_scale=float(fx["scale"]),
+                                     causal=True)
+    torch.cuda.synchronize()
+    absv = oracle.varlen_attention(fx["q"], fx["k"], np.abs(oracle.bf16_bits_to_f32(fx["v"])),
+                                   fx["cu_seqlens"], scale=float(fx["scale"]))
+    check_attention(out, fx["out"], what="tiny prefill", absv=absv)
+
+
+def test_prefill_8x1024_with_store_full_size(gpu):
+    # Qwen3-0.6B attention shape: 16/8 heads, D=128, 8 packed sequences of
+    # 1024 tokens; q/k/v ~ N(0,1) bf16 with v a strided view of the fused qkv
+    # buffer; K/V written into a paged cache (block 256, shuffled ids) through
+    # slot_mapping in the same call.
+    print("case: prefill 8x1024 + store", flush=True)
+    N, hq, hkv, d, bs = 8192, 16, 8, 128, 256
+    g = torch.Generator(device=gpu).manual_seed(0)
+    qkv = torch.randn((N, (hq + 2 * hkv) * d), generator=g, device=gpu).to(torch.bfloat16)
+    q = qkv[:, :hq * d].view(N, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(N, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(N, hkv, d)
+    rs = np.random.RandomState(0)
+    perm = rs.permutation(40).astype(np.int32)  # 32 blocks used out of 40
+    bt = perm[:32].reshape(8, 4)
+    cu, _, sm = paged.build_prefill_metadata([1024] * 8, bt, bs, gpu)
+    kc = torch.randn((40, bs, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+    vc = torch.randn((40, bs, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+    kc_ref, vc_ref = np_of(kc).copy(), np_of(vc).copy()
+    out = fai.varlen_prefill_with_kvcache(q, k, v, cu, 1024, kc, vc, sm,
+                                          softmax_scale=d ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    sm_np = sm.cpu().numpy()
+    oracle.kv_store(kc_ref, np_of(k), sm_np)
+    oracle.kv_store(vc_ref, np_of(v), sm_np)
+    assert np.array_equal(bytes_of(kc), kc_ref.view(np.uint8))
+    assert np.array_equal(bytes_of(vc), vc_ref.view(np.uint8))
+    cu_np = cu.cpu().numpy()
+    ref = oracle.varlen_attention(f64(q), f64(k), f64(v), cu_np, scale=d ** -0.5)
+    absv = oracle.varlen_attention(f64(q), f64(k), np.abs(f64(v)), cu_np, scale=d ** -0.5)
+    err = check_attention(out, ref, what="prefill 8x1024", absv=absv)
+    print(f"max-abs err {err:.3e}", flush=True)
+
+
+def _ragged(lens_q, lens_k, hq, hkv, dtype, gpu, seed):
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    nq, nk = sum(lens_q), sum(lens_k)
+    q = torch.randn((nq, hq, 128), generator=g, device=gpu).to(dtype)
+    k = torch.randn((nk, hkv, 128), generator=g, device=gpu).to(dtype)
+    v = torch.randn((nk, hkv, 128), generator=g, device=gpu).to(dtype)
+    cq = torch.tensor(np.concatenate([[0], np.cumsum(lens_q)]), dtype=torch.int32, device=gpu)
+    ck = torch.tensor(np.concatenate([[0], np.cumsum(lens_k)]), dtype=torch.int32, device=gpu)
+    return q, k, v, cq, ck
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_ragged_groups_dtypes(gpu, hq, hkv, dtype, causal):
+    print(f"case: ragged {hq}/{hkv} {dtype} causal={causal}", flush=True)
+    lens = [1, 5, 31, 32, 33, 0, 127, 128, 129, 300, 64]
+    q, k, v, cq, _ = _ragged(lens, lens, hq, hkv, dtype, gpu, 1)
+    out = fai.flash_attn_varlen_func(q, k, v, cq, cq, max(lens), max(lens), softmax_scale=0.1,
+                                     causal=causal)
+    torch.cuda.synchronize()
+    ref = oracle.varlen_attention(f64(q), f64(k), f64(v), cq.cpu().numpy(), scale=0.1,
+                                  causal=causal)
+    absv = oracle.varlen_attention(f64(q), f64(k), np.abs(f64(v)), cq.cpu().numpy(), scale=0.1,
+                                   causal=causal)
+    check_attention(out, ref, what="ragged", absv=absv)
+
+
+def test_prefill_bottom_right_causal_lq_ne_lk(gpu):
+    # chunked-prefill shape: fewer queries than keys per segment (and one
+    # segment with more queries than keys, whose first rows see nothing)
+    print("case: lq != lk", flush=True)
+    lq, lk = [5, 100, 64, 40], [70, 100, 300, 20]
+    q, k, v, cq, ck = _ragged(lq, lk, 16, 8, torch.bfloat16, gpu, 2)
+    out = fai.flash_attn_varlen_func(q, k, v, cq, ck, max(lq), max(lk), causal=True)
+    torch.cuda.synchronize()
+    ref = oracle.varlen_attention(f64(q), f64(k), f64(v), cq.cpu().numpy(), ck.cpu().numpy(),
+                                  causal=True)
+    absv = oracle.varlen_attention(f64(q), f64(k), np.abs(f64(v)), cq.cpu().numpy(),
+                                   ck.cpu().numpy(), causal=True)
+    check_attention(out, ref, what="lq != lk", absv=absv)
+    assert not out[cq[3].item():cq[3].item() + 20].any()  # rows with no visible key
+
+
+def test_flash_attn_func_padded_batch(gpu):
+    print("case: padded flash_attn_func", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(3)
+    B, T = 3, 200
+    q = torch.randn((B, T, 16, 128), generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn((B, T, 8, 128), generator=g, device=gpu).to(torch.bfloat16)
+    v = torch.randn((B, T, 8, 128), generator=g, device=gpu).to(torch.bfloat16)
+    out = fai.flash_attn_func(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    cu = np.arange(0, (B + 1) * T, T, dtype=np.int32)
+    qf, kf, vf = (f64(t).reshape(B * T, -1, 128) for t in (q, k, v))
+    ref = oracle.varlen_attention(qf, kf, vf, cu)
+    absv = oracle.varlen_attention(qf, kf, np.abs(vf), cu)
+    check_attention(out.reshape(B * T, 16, 128), ref, what="padded", absv=absv)
+
+
+def test_decode_equals_last_prefill_row(gpu):
+    # invariant: a causal prefill's row i equals a decode over keys 0..i
+    print("case: decode == prefill row", flush=True)
+    L, hq, hkv, bs = 300, 16, 8, 64
+    q, k, v, cq, _ = _ragged([L], [L], hq, hkv, torch.bfloat16, gpu, 4)
+    pre = fai.flash_attn_varlen_func(q, k, v, cq, cq, L, L, causal=True)
+    nb = (L + bs - 1) // bs
+    kc = torch.zeros((nb, bs, hkv, 128), dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros_like(kc)
+    bt = torch.arange(nb, dtype=torch.int32, device=gpu).view(1, nb)
+    sm = torch.arange(L, dtype=torch.int64, device=gpu)
+    fai.kv_store(k, v, kc, vc, sm)
+    rows = [0, 63, 64, 299]
+    dec = fai.decode_paged(q[rows].contiguous(), kc, vc, bt.expand(len(rows), nb).contiguous(),
+                           torch.tensor([r + 1 for r in rows], dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+    diff = (dec.float() - pre[rows].float()).abs().max().item()
+    assert diff <= 2 ** -7, diff
