@@ -1,0 +1,291 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention hot path on one MI355X.
+
+Default workload (the N=1 `value`): single-layer paged decode at the Qwen3
+serving shape -- 256 sequences, 16 query / 8 KV heads, head_dim 128, bf16,
+context ~ U[1024, 2047] after the store, KV block 256 with block tables drawn
+from one shuffled shared pool.  One step = store one new K/V token per
+sequence through the paged append, then attend (flash_attn_with_kvcache with
+k=/v=).  `value` is the step's algorithmic HBM bytes (K/V context read once,
+q read, output written, new K/V read and stored) divided by the step time,
+inputs resident in HBM.
+
+Also reported on the same line:
+  roofline      the decode attention launch alone (aac_decode_paged), timed
+                with HIP events on the launch stream, against 8 TB/s HBM;
+  prefill       varlen causal prefill, 8 x 1024 tokens, 16/8 heads, bf16, with
+                the paged store in the same call, as TFLOP/s against the
+                2.5 PFLOP/s dense bf16 MFMA peak (roofline of that kernel);
+  cpu_baseline  the numpy oracle on a bounded sample of the decode workload,
+                single-threaded on the host cores.
+
+`python bench.py --gpus N --steps K --warmup W`; only N=1 is supported (one
+GPU), N>1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--partition", type=int, default=0, help="decode partition tokens (0=auto)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--only", choices=["decode", "prefill"], default=None,
+                   help="run one leg only (for profiling)")
+    return p.parse_args()
+
+
+# ----------------------------------------------------------------------------
+# decode: 256 seqs x ctx U[1024, 2047]
+# ----------------------------------------------------------------------------
+def make_decode_inputs(torch, dev, seed, B=256, hq=16, hkv=8, d=128, bs=256):
+    rs = np.random.RandomState(seed)
+    ctx = rs.randint(1024, 2048, B).astype(np.int32)          # after the store
+    need = [int(-(-c // bs)) for c in ctx]
+    pool = sum(need)
+    perm = rs.permutation(pool).astype(np.int32)
+    width = max(need)
+    bt = np.zeros((B, width), np.int32)
+    k0 = 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[k0:k0 + n]
+        k0 += n
+    g = torch.Generator(device=dev).manual_seed(seed)
+    bf = torch.bfloat16
+    kc = torch.randn((pool, bs, hkv, d), generator=g, device=dev).to(bf)
+    vc = torch.randn((pool, bs, hkv, d), generator=g, device=dev).to(bf)
+    q = torch.randn((B, 1, hq, d), generator=g, device=dev).to(bf)
+    kn = torch.randn((B, 1, hkv, d), generator=g, device=dev).to(bf)
+    vn = torch.randn((B, 1, hkv, d), generator=g, device=dev).to(bf)
+    return dict(ctx=ctx, bt=bt, kc=kc, vc=vc, q=q, kn=kn, vn=vn, B=B, hq=hq, hkv=hkv, d=d, bs=bs,
+                bt_g=torch.from_numpy(bt).to(dev),
+                seqlens_g=torch.from_numpy(ctx - 1).to(dev),
+                ctx_g=torch.from_numpy(ctx).to(dev))
+
+
+def decode_bytes(x):
+    kv = int(x["ctx"].sum()) * x["hkv"] * x["d"] * 2 * 2
+    qo = 2 * x["B"] * x["hq"] * x["d"] * 2
+    store = 2 * x["B"] * x["hkv"] * x["d"] * 2 * 2  # new k/v read + written
+    return kv + qo, kv + qo + store
+
+
+def bench_decode(torch, fai, dev, args):
+    x = make_decode_inputs(torch, dev, args.seed)
+    attend_bytes, step_bytes = decode_bytes(x)
+    maxctx = int(x["ctx"].max())
+
+    def step():
+        return fai.flash_attn_with_kvcache(
+            x["q"], x["kc"], x["vc"], k=x["kn"], v=x["vn"], cache_seqlens=x["seqlens_g"],
+            block_table=x["bt_g"], causal=False, max_context_len=maxctx)
+
+    q3 = x["q"].view(x["B"], x["hq"], x["d"])
+    out3 = torch.empty_like(q3)
+
+    def attend():
+        return fai.decode_paged(q3, x["kc"], x["vc"], x["bt_g"], x["ctx_g"],
+                                max_context_len=maxctx, partition_tokens=args.partition,
+                                out=out3)
+
+    for _ in range(args.warmup):
+        step()
+        attend()
+    torch.cuda.synchronize()
+    # whole step (store + attend), wall clock
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t_step = (time.perf_counter() - t0) / args.steps
+    # the attention launch alone, HIP events on the launch stream
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        a.record()
+        attend()
+        b.record()
+    torch.cuda.synchronize()
+    t_att = sum(a.elapsed_time(b) for a, b in evs) / len(evs) / 1e3
+    achieved = attend_bytes / t_att / 1e9
+    return dict(
+        t_step=t_step, step_bytes=step_bytes, attend_bytes=attend_bytes, t_attend=t_att,
+        achieved=achieved, x=x)
+
+
+# ----------------------------------------------------------------------------
+# prefill: 8 x 1024 causal, 16/8 heads, store in the same call
+# ----------------------------------------------------------------------------
+def bench_prefill(torch, fai, paged, dev, args):
+    N, hq, hkv, d, bs, nseq, L = 8192, 16, 8, 128, 256, 8, 1024
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    qkv = torch.randn((N, (hq + 2 * hkv) * d), generator=g, device=dev).to(torch.bfloat16)
+    q = qkv[:, :hq * d].view(N, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].contiguous().view(N, hkv, d)  # post-RoPE copy
+    v = qkv[:, (hq + hkv) * d:].view(N, hkv, d)                      # strided view
+    rs = np.random.RandomState(args.seed)
+    perm = rs.permutation(32).astype(np.int32)
+    cu, _, sm = paged.build_prefill_metadata([L] * nseq, perm.reshape(nseq, 4), bs, dev)
+    kc = torch.zeros((32, bs, hkv, d), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    flops = 4 * hq * d * nseq * (L * (L + 1) // 2)
+
+    def step():
+        return fai.varlen_prefill_with_kvcache(q, k, v, cu, L, kc, vc, sm, causal=True)
+
+    def attend():
+        return fai.flash_attn_varlen_func(q, k, v, cu, cu, L, L, causal=True)
+
+    for _ in range(args.warmup):
+        step()
+        attend()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t_step = (time.perf_counter() - t0) / args.steps
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for a, b in evs:
+        a.record()
+        attend()
+        b.record()
+    torch.cuda.synchronize()
+    t_att = sum(a.elapsed_time(b) for a, b in evs) / len(evs) / 1e3
+    return dict(t_step=t_step, t_attend=t_att, flops=flops, tflops=flops / t_att / 1e12)
+
+
+# ----------------------------------------------------------------------------
+# CPU baseline: the oracle on a bounded sample of the decode workload
+# ----------------------------------------------------------------------------
+def cpu_baseline(x, reps=3, seed=1):
+    """The oracle's store-then-attend over the same decode shape (all 256
+    sequences, the same context lengths), single-threaded; best of ``reps``."""
+    import oracle
+    from threadpoolctl import threadpool_limits
+
+    rng = np.random.default_rng(seed)
+    hq, hkv, d, bs = x["hq"], x["hkv"], x["d"], x["bs"]
+    ctx = x["ctx"]
+    B = ctx.shape[0]
+    need = [int(-(-c // bs)) for c in ctx]
+    pool = sum(need)
+    bt = np.zeros((B, max(need)), np.int32)
+    perm = rng.permutation(pool).astype(np.int32)
+    k0 = 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[k0:k0 + n]
+        k0 += n
+
+    def bf16(shape):  # bf16 bit patterns of values with |x| in [2^-7, 4), random sign
+        n = int(np.prod(shape))
+        bits = rng.integers(0x3C00, 0x4080, n, dtype=np.uint16)
+        bits |= rng.integers(0, 2, n, dtype=np.uint16) << np.uint16(15)
+        return bits.reshape(shape)
+
+    kc, vc = bf16((pool, bs, hkv, d)), bf16((pool, bs, hkv, d))
+    q, kn, vn = bf16((B, hq, d)), bf16((B, hkv, d)), bf16((B, hkv, d))
+    best = float("inf")
+    with threadpool_limits(limits=1):
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            oracle.decode_append_attend(q, kc, vc, kn, vn, bt, ctx - 1, bs)
+            best = min(best, time.perf_counter() - t0)
+    nbytes = decode_bytes(dict(ctx=ctx, B=B, hq=hq, hkv=hkv, d=d))[1]
+    return dict(value=round(nbytes / best / 1e9, 4), unit="GB/s", cores=1, kind="port",
+                sample=f"oracle.decode_append_attend (numpy, float64 math, 1 thread): the full "
+                       f"store+attend step over all {B} sequences ({int(ctx.sum())} context "
+                       f"tokens), best of {reps} runs",
+                seconds_per_step=round(best, 3))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the attention path shards by sequence or KV head with no exchange; "
+              "the figure at N GPUs is N independent copies of the N=1 line)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from awesome_acceleration_amd import flash_attn_interface as fai, paged
+
+    dev = torch.device("cuda:0")
+    res = {}
+    if args.only in (None, "decode"):
+        res["decode"] = bench_decode(torch, fai, dev, args)
+    if args.only in (None, "prefill") and not args.no_prefill:
+        res["prefill"] = bench_prefill(torch, fai, paged, dev, args)
+    if args.only is not None:
+        print(json.dumps({k: {kk: vv for kk, vv in v.items() if kk != "x"}
+                          for k, v in res.items()}, default=float))
+        return
+    dec = res["decode"]
+    line = {
+        "metric": "decode-attn HBM GB/s + prefill MFMA util; Qwen3-0.6B output tok/s @1 GPU",
+        "value": round(dec["step_bytes"] / dec["t_step"] / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["t_step"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v and caches, random shuffled block tables)",
+        "config": {
+            "workload": "paged decode store+attend, 256 seqs, 16 q / 8 kv heads, head_dim 128, "
+                        "context U[1024,2047], block 256, shared shuffled pool",
+            "seqs": 256, "q_heads": 16, "kv_heads": 8, "head_dim": 128, "block_size": 256,
+            "context_tokens": int(dec["x"]["ctx"].sum()),
+            "step_bytes": dec["step_bytes"],
+        },
+        "roofline": {
+            "kernel": "decode attention (aac_decode_paged: partition kernel + LSE reduce)",
+            "bound": "hbm",
+            "achieved": round(dec["achieved"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dec["achieved"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": dec["attend_bytes"],
+            "us_per_launch": round(dec["t_attend"] * 1e6, 2),
+        },
+    }
+    if "prefill" in res:
+        pf = res["prefill"]
+        line["prefill"] = {
+            "workload": "varlen causal prefill 8 x 1024 tokens, 16/8 heads, head_dim 128, bf16",
+            "us_attend": round(pf["t_attend"] * 1e6, 2),
+            "us_step_with_store": round(pf["t_step"] * 1e6, 2),
+            "roofline": {"bound": "mfma", "achieved": round(pf["tflops"], 2),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(pf["tflops"] / BF16_PEAK_TFLOPS, 4),
+                         "flops_per_launch": pf["flops"], "traffic": None},
+        }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(dec["x"])
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
