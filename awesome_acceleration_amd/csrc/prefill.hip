@@ -3,11 +3,12 @@
 // call (llm.py:178-184), and with the store folded in, llm.py:171-184.
 //
 // Tiling (FlashAttention-2 style, Dao 2023, re-derived for CDNA4 MFMA):
-//   * A workgroup (4 wavefronts) owns one KV head h of one segment and a block
-//     of BQ queries for all G = Hq/Hkv query heads that read h.  Wave w serves
-//     32 queries x HPW (<= 2) heads; with G = 2 the four waves cover 128
-//     queries x 2 heads, so every K/V tile staged in LDS feeds 2 heads x 128
-//     queries (the KV head is shared across its query heads).
+//   * A workgroup (8 wavefronts, 2 per SIMD) owns one KV head h of one
+//     segment and a block of BQ queries for all G = Hq/Hkv query heads that
+//     read h.  Wave w serves 32 queries of one head; with G = 2 the eight
+//     waves cover 128 queries x 2 heads, so every K/V tile staged in LDS feeds
+//     2 heads x 128 queries (the KV head is shared across its query heads).
+//     Two waves per SIMD let one wave's MFMAs overlap the other's softmax.
 //   * Scores are computed transposed, S^T = K Q^T, with
 //     v_mfma_f32_32x32x16_{bf16,f16}: A = 32 keys x 16 dims read from LDS,
 //     B = 16 dims x 32 queries held in registers for the whole kernel.  The
@@ -18,7 +19,10 @@
 //   * The probabilities, rounded to bf16, are already laid out as the B operand
 //     of O^T += V^T P^T (B[k][n] sits in lane n + 32*(k/8)); V^T comes from an
 //     LDS tile that is written transposed ([dim][key]) when it is staged.
-//   * Online softmax in fp32 in the log2 domain (exp via v_exp_f32).
+//   * Online softmax in fp32 in the log2 domain (exp via v_exp_f32) with
+//     lazy rescaling (the running max used for the exponent only moves when a
+//     row max exceeds it by more than 2^8, as in FlashAttention-3), so the
+//     accumulators are rarely touched by VALU work.
 //   * Causal masking is bottom-right aligned (query i sees keys
 //     j <= i + Lk - Lq); key tiles beyond a wave's last visible key are
 //     skipped, and only tiles that cross the diagonal evaluate the mask.
@@ -35,9 +39,12 @@ namespace aac {
 namespace pf {
 
 constexpr int D = 128;
-constexpr int BKV = 64;         // keys per LDS tile
-constexpr int KPITCH = D + 8;   // K tile row pitch (elements)
-constexpr int VPITCH = BKV + 8; // V^T tile row pitch (elements)
+constexpr int BKV = 64;        // keys per LDS tile (two 32-key sub-tiles)
+constexpr int KPITCH = D + 8;  // K tile row pitch (elements): 8 consecutive rows hit 8 disjoint bank quads
+constexpr int STAGES = 3;      // LDS ring: one barrier per tile (see the hazard note in the kernel)
+constexpr float kRescale = 8.f;  // lazy-rescale threshold (log2 units): p <= 256
+constexpr int kWaves = 8;        // wavefronts per workgroup (2 per SIMD)
+constexpr int kThreads = 64 * kWaves;
 
 struct Args {
   const u16* q;
@@ -58,7 +65,10 @@ template <> struct Mfma<false> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-  __device__ static inline u32 pack(float a, float b) { return pack_bf16x2(a, b); }
+  __device__ static inline u32 pack(float a, float b) {
+    typedef __attribute__((ext_vector_type(2))) float f2;
+    return __builtin_bit_cast(u32, __builtin_convertvector((f2){a, b}, bf16x2));
+  }
 };
 template <> struct Mfma<true> {
   __device__ static inline f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
@@ -72,17 +82,35 @@ template <> struct Mfma<true> {
 constexpr u32 kSelLo = 0x05040100u;  // (lo16 of lo_src, lo16 of hi_src)
 constexpr u32 kSelHi = 0x07060302u;  // (hi16 of lo_src, hi16 of hi_src)
 
+// V^T tile layout: 128 rows (dims) x 64 keys, no padding.  Keys are handled
+// in quads (4 keys = 8 bytes).  Inside each 16-key group the quad order is
+// (0,2,1,3) so that the 8 keys one lane half feeds to an MFMA (keys
+// 4h..4h+3 and 8+4h..8+4h+3 of the group) are one contiguous 16-byte octet;
+// the 8 octets of a row are XOR-swizzled by (row ^ row>>3) & 7 so that both
+// the b128 reads (8 consecutive rows, same octet) and the b64 writes (rows
+// 8*i + c, same quad) spread over the banks.
+__device__ __forceinline__ int vt_quad_off(int row, int quad) {
+  const int g = quad >> 2, qq = quad & 3;
+  const int pq = (g << 2) | ((qq & 1) << 1) | (qq >> 1);
+  const int oct = (pq >> 1) ^ ((row ^ (row >> 3)) & 7);
+  return row * BKV + oct * 8 + (pq & 1) * 4;
+}
+// element offset of the octet holding keys {16*g + 4*hl + 0..3, 16*g + 8 + 4*hl + 0..3}
+__device__ __forceinline__ int vt_octet_off(int row, int g, int hl) {
+  return row * BKV + (((2 * g + hl) ^ ((row ^ (row >> 3)) & 7)) * 8);
+}
+
 template <int G, bool CAUSAL, bool F16>
-__global__ __launch_bounds__(256) void prefill_kernel(Args a) {
-  constexpr int HPW = G >= 2 ? 2 : 1;  // query heads per wave
+__global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
+  constexpr int HPW = 1;               // query heads per wave
   constexpr int WH = G / HPW;          // head slots per workgroup
-  constexpr int WQ = 4 / WH;           // 32-query slots per workgroup
+  constexpr int WQ = kWaves / WH;      // 32-query slots per workgroup
   constexpr int BQ = 32 * WQ;
-  static_assert(WH * WQ == 4, "four waves per workgroup");
+  static_assert(WH * WQ == kWaves, "eight waves per workgroup");
   typedef Mfma<F16> M;
 
-  __shared__ __attribute__((aligned(16))) u16 Ks[BKV * KPITCH];
-  __shared__ __attribute__((aligned(16))) u16 Vt[D * VPITCH];
+  __shared__ __attribute__((aligned(16))) u16 Ks[STAGES][BKV * KPITCH];
+  __shared__ __attribute__((aligned(16))) u16 Vt[STAGES][D * BKV];
 
   const int h = blockIdx.x;
   const int s = blockIdx.y;
@@ -106,23 +134,26 @@ __global__ __launch_bounds__(256) void prefill_kernel(Args a) {
   const int kv_end = CAUSAL ? max(0, min(Lk, wg_qmax + 1 + shift)) : Lk;
   const int w_qmin = qb * BQ + wq * 32;
   const int w_qmax = min(w_qmin + 31, Lq - 1);
-  const int w_end = CAUSAL ? max(0, min(Lk, w_qmax + 1 + shift)) : Lk;
+  const int w_end = w_qmin >= Lq ? 0 : (CAUSAL ? max(0, min(Lk, w_qmax + 1 + shift)) : Lk);
   const int w_full = CAUSAL ? min(Lk, w_qmin + 1 + shift) : Lk;  // keys < w_full need no mask
   const int my_lim = CAUSAL ? min(Lk, qi + 1 + shift) : Lk;
+  const int nt = (kv_end + BKV - 1) / BKV;  // LDS tiles (workgroup-uniform)
+  const int nsub = (w_end + 31) / 32;       // 32-key sub-tiles this wave computes
 
   // Q fragments: B operand of S^T = K Q^T, lane = query column, 8 dims.
   u32x4 qf[HPW][8];
+  {
+    const int qrow = q_beg + min(qi, max(Lq - 1, 0));  // clamped: rows >= Lq are never stored
 #pragma unroll
-  for (int j = 0; j < HPW; ++j) {
-    const int hq = h * G + wh * HPW + j;
-    const u16* qp = a.q + (int64_t)(q_beg + qi) * a.q_stride + hq * D + hl * 8;
+    for (int j = 0; j < HPW; ++j) {
+      const u16* qp = a.q + (int64_t)qrow * a.q_stride + (h * G + wh * HPW + j) * D + hl * 8;
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-      qf[j][t] = q_ok ? *reinterpret_cast<const u32x4*>(qp + 16 * t) : u32x4{0, 0, 0, 0};
+      for (int t = 0; t < 8; ++t) qf[j][t] = *reinterpret_cast<const u32x4*>(qp + 16 * t);
+    }
   }
 
   f32x16 o[HPW][4];
-  float m[HPW], l[HPW];
+  float m[HPW], l[HPW];  // m: running max of the raw scores (scale applied in exp2)
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
     m[j] = -1e30f;
@@ -133,110 +164,166 @@ __global__ __launch_bounds__(256) void prefill_kernel(Args a) {
       for (int i = 0; i < 16; ++i) o[j][c][i] = 0.f;
   }
 
-  const u16* kg = a.k + (int64_t)k_beg * a.k_stride + h * D;
-  const u16* vg = a.v + (int64_t)k_beg * a.v_stride + h * D;
+  // Staging: waves 0-3 stage K (thread loads rows (tid>>4) + 16*i), waves
+  // 4-7 stage V (thread loads rows 4*(tid>>4) + i, transposed into V^T), 16 B
+  // at dim (tid&15)*8.  Rows past kv_end are clamped to the last visible row
+  // (finite data; those keys are masked, so p = 0 multiplies it).
+  const bool k_role = tid < 256;
+  const int st_r = (tid & 255) >> 4, st_c = (tid & 15) * 8;
+  const u16* sg = k_role ? a.k + (int64_t)k_beg * a.k_stride + h * D + st_c
+                         : a.v + (int64_t)k_beg * a.v_stride + h * D + st_c;
+  const int64_t sg_stride = k_role ? a.k_stride : a.v_stride;
+  const int last = max(kv_end - 1, 0);
+  u32x4 sp[4];
 
-  for (int kt = 0; kt < kv_end; kt += BKV) {
-    __syncthreads();
-    // ---- stage K tile [BKV][D] (row pitch KPITCH)
+  // per-lane LDS read offsets (elements)
+  const int k_rd = col * KPITCH + hl * 8;
+  int v_row[4], v_x[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int row = 32 * c + col;
+    v_row[c] = row * BKV;
+    v_x[c] = hl ^ ((row ^ (row >> 3)) & 7);
+  }
+
+  auto prefetch = [&](int t) {
+    const int k0 = t * BKV;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int chunk = tid + 256 * i;
-      const int r = chunk >> 4, c8 = (chunk & 15) * 8;
-      u32x4 val = {0, 0, 0, 0};
-      if (kt + r < kv_end) val = *reinterpret_cast<const u32x4*>(kg + (int64_t)(kt + r) * a.k_stride + c8);
-      *reinterpret_cast<u32x4*>(Ks + r * KPITCH + c8) = val;
+      const int r = k_role ? k0 + st_r + 16 * i : k0 + st_r * 4 + i;
+      sp[i] = *reinterpret_cast<const u32x4*>(sg + (int64_t)min(r, last) * sg_stride);
     }
-    // ---- stage V^T tile [D][BKV]: thread = 4 keys x 8 dims, transposed in registers
-    {
-      const int kq = tid >> 4;       // key quad 0..15
-      const int d0 = (tid & 15) * 8;  // first dim
-      u32x4 r[4];
+  };
+  auto stage_write = [&](int t) {
+    if (k_role) {
+      u16* ks = Ks[t % STAGES];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kt + kq * 4 + i;
-        r[i] = key < kv_end ? *reinterpret_cast<const u32x4*>(vg + (int64_t)key * a.v_stride + d0)
-                            : u32x4{0, 0, 0, 0};
-      }
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<u32x4*>(ks + (st_r + 16 * i) * KPITCH + st_c) = sp[i];
+    } else {
+      u16* vt = Vt[t % STAGES];
 #pragma unroll
-      for (int jw = 0; jw < 4; ++jw) {  // dims d0+2jw (lo) and d0+2jw+1 (hi)
+      for (int jw = 0; jw < 4; ++jw) {  // dims st_c+2jw (lo halves) and st_c+2jw+1 (hi halves)
         u32x2 lo, hi;
-        lo[0] = __builtin_amdgcn_perm(r[1][jw], r[0][jw], kSelLo);
-        lo[1] = __builtin_amdgcn_perm(r[3][jw], r[2][jw], kSelLo);
-        hi[0] = __builtin_amdgcn_perm(r[1][jw], r[0][jw], kSelHi);
-        hi[1] = __builtin_amdgcn_perm(r[3][jw], r[2][jw], kSelHi);
-        *reinterpret_cast<u32x2*>(Vt + (d0 + 2 * jw) * VPITCH + kq * 4) = lo;
-        *reinterpret_cast<u32x2*>(Vt + (d0 + 2 * jw + 1) * VPITCH + kq * 4) = hi;
+        lo[0] = __builtin_amdgcn_perm(sp[1][jw], sp[0][jw], kSelLo);
+        lo[1] = __builtin_amdgcn_perm(sp[3][jw], sp[2][jw], kSelLo);
+        hi[0] = __builtin_amdgcn_perm(sp[1][jw], sp[0][jw], kSelHi);
+        hi[1] = __builtin_amdgcn_perm(sp[3][jw], sp[2][jw], kSelHi);
+        *reinterpret_cast<u32x2*>(vt + vt_quad_off(st_c + 2 * jw, st_r)) = lo;
+        *reinterpret_cast<u32x2*>(vt + vt_quad_off(st_c + 2 * jw + 1, st_r)) = hi;
       }
     }
-    __syncthreads();
-
+  };
+  // S^T for 32-key sub-tile j (keys 32j..32j+31) of every head of this wave
+  auto scores = [&](int j, f32x16* st) {
+    const u16* kr = Ks[(j >> 1) % STAGES] + (j & 1) * 32 * KPITCH + k_rd;
 #pragma unroll
-    for (int sub = 0; sub < BKV / 32; ++sub) {
-      const int kb = kt + sub * 32;
-      if (kb >= w_end) break;  // wave-uniform
-      // ---- S^T = K Q^T for HPW heads
-      f32x16 st[HPW];
+    for (int x = 0; x < HPW; ++x)
 #pragma unroll
-      for (int j = 0; j < HPW; ++j)
+      for (int i = 0; i < 16; ++i) st[x][i] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) st[j][i] = 0.f;
-      const u16* kr = Ks + (sub * 32 + col) * KPITCH + hl * 8;
+    for (int t = 0; t < 8; ++t) {
+      const u32x4 ka = *reinterpret_cast<const u32x4*>(kr + 16 * t);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const u32x4 ka = *reinterpret_cast<const u32x4*>(kr + 16 * t);
+      for (int x = 0; x < HPW; ++x) st[x] = M::run(ka, qf[x][t], st[x]);
+    }
+  };
+  // online softmax of one sub-tile (log2 domain, raw-score running max);
+  // returns P^T as the B operand of the PV product
+  auto softmax = [&](int j, f32x16* st, u32x4 (*pb)[2], bool first) {
+    const int kb = 32 * j;
+    const bool need_mask = kb + 32 > w_full;  // wave-uniform
 #pragma unroll
-        for (int j = 0; j < HPW; ++j) st[j] = M::run(ka, qf[j][t], st[j]);
+    for (int x = 0; x < HPW; ++x) {
+      if (need_mask) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + 8 * (i >> 2) + 4 * hl + (i & 3);
+          st[x][i] = key < my_lim ? st[x][i] : -INFINITY;
+        }
       }
-      const bool need_mask = kb + 32 > w_full;  // wave-uniform
-      // ---- online softmax (log2 domain); P^T packed as the PV B operand
-      u32x4 pb[HPW][2];
+      float mx = fmaxf(st[x][0], st[x][1]);
 #pragma unroll
-      for (int j = 0; j < HPW; ++j) {
-        float sv[16];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float x = st[j][i] * a.scale_log2;
-          if (need_mask) {
-            const int key = kb + 8 * (i >> 2) + 4 * hl + (i & 3);
-            x = key < my_lim ? x : -INFINITY;
-          }
-          sv[i] = x;
-          mx = fmaxf(mx, x);
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mn = fmaxf(m[j], mx);
-        const float alpha = fast_exp2(m[j] - mn);
-        m[j] = mn;
-        float ps = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          sv[i] = fast_exp2(sv[i] - mn);
-          ps += sv[i];
-        }
-        l[j] = l[j] * alpha + ps;
+      for (int i = 2; i < 16; ++i) mx = fmaxf(mx, st[x][i]);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                       false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      // Lazy rescaling: the reference max m only moves when some row's max
+      // exceeds it by more than kRescale (log2 units), so p <= 2^kRescale and
+      // the O/l accumulators (exactly normalised at the end) are rescaled
+      // rarely; on the first sub-tile they are still zero.
+      const float grow = (mx - m[x]) * a.scale_log2;
+      if (first) {
+        m[x] = fmaxf(mx, -1e30f);
+      } else if (__any(grow > kRescale)) {
+        const float mn = fmaxf(m[x], mx);
+        const float alpha = fast_exp2((m[x] - mn) * a.scale_log2);
+        m[x] = mn;
+        l[x] *= alpha;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) o[j][c][i] *= alpha;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) pb[j][t][w] = M::pack(sv[8 * t + 2 * w], sv[8 * t + 2 * w + 1]);
+          for (int i = 0; i < 16; ++i) o[x][c][i] *= alpha;
       }
-      // ---- O^T += V^T P^T  (A = V^T rows: dims; k: keys in the lane-half order)
+      const float nb = -m[x] * a.scale_log2;
+      float p[16];
+      float ps = 0.f;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u16* vr = Vt + (32 * c + col) * VPITCH + sub * 32 + 4 * hl;
+      for (int i = 0; i < 16; ++i) {
+        p[i] = fast_exp2(fmaf(st[x][i], a.scale_log2, nb));
+        ps += p[i];
+      }
+      l[x] += ps;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const u32x2 v0 = *reinterpret_cast<const u32x2*>(vr + 16 * t);
-          const u32x2 v1 = *reinterpret_cast<const u32x2*>(vr + 16 * t + 8);
-          const u32x4 va = {v0[0], v0[1], v1[0], v1[1]};
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int j = 0; j < HPW; ++j) o[j][c] = M::run(va, pb[j][t], o[j][c]);
-        }
+        for (int w = 0; w < 4; ++w) pb[x][tt][w] = M::pack(p[8 * tt + 2 * w], p[8 * tt + 2 * w + 1]);
+    }
+  };
+  auto pv = [&](int j, u32x4 (*pb)[2]) {
+    const u16* vt = Vt[(j >> 1) % STAGES];
+    const int g0 = 2 * (j & 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const u32x4 va =
+            *reinterpret_cast<const u32x4*>(vt + v_row[c] + ((v_x[c] ^ (2 * (g0 + tt))) << 3));
+#pragma unroll
+        for (int x = 0; x < HPW; ++x) o[x][c] = M::run(va, pb[x][tt], o[x][c]);
+      }
+    }
+  };
+
+  // Prologue: tile 0 in LDS, tile 1 in flight, S of sub-tile 0.
+  f32x16 sc[HPW];
+  if (nt > 0) {
+    prefetch(0);
+    stage_write(0);
+    if (nt > 1) prefetch(1);
+    __syncthreads();
+    if (nsub > 0) scores(0, sc);
+  }
+
+  // Ring hazard: tile t+1 is written to stage (t+1)%3 after the barrier of
+  // iteration t-1, which every wave reaches only after it has finished all
+  // reads of tile t-2 (the last reader of that stage); the barrier of
+  // iteration t makes tile t+1 visible before the look-ahead scores read it.
+  for (int t = 0; t < nt; ++t) {
+    if (t + 1 < nt) stage_write(t + 1);
+    __syncthreads();
+    if (t + 2 < nt) prefetch(t + 2);
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int j = 2 * t + sub;
+      if (j < nsub) {  // wave-uniform
+        f32x16 sn[HPW];
+        if (j + 1 < nsub) scores(j + 1, sn);
+        u32x4 pb[HPW][2];
+        softmax(j, sc, pb, j == 0);
+        pv(j, pb);
+#pragma unroll
+        for (int x = 0; x < HPW; ++x) sc[x] = sn[x];
       }
     }
   }
@@ -264,10 +351,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(Args a) {
 
 template <int G, bool CAUSAL, bool F16>
 static void launch_t(const Args& a, int max_q, hipStream_t st) {
-  constexpr int HPW = G >= 2 ? 2 : 1;
-  constexpr int BQ = 32 * (4 / (G / HPW));
+  constexpr int BQ = 32 * (kWaves / G);
   dim3 grid(a.hkv, a.n_seqs, (unsigned)cdiv(max_q, BQ));
-  hipLaunchKernelGGL((prefill_kernel<G, CAUSAL, F16>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((prefill_kernel<G, CAUSAL, F16>), grid, dim3(kThreads), 0, st, a);
 }
 
 template <bool CAUSAL, bool F16>
