@@ -32,6 +32,8 @@
 // FLOPs per launch (the MFMA roofline): 4 * Hq * D * sum over segments of the
 // visible (query, key) pairs, i.e. 4*Hq*D*L(L+1)/2 per causal segment.
 
+#include <algorithm>
+
 #include "aac_common.h"
 
 namespace aac {
@@ -69,6 +71,10 @@ template <> struct Mfma<false> {
     typedef __attribute__((ext_vector_type(2))) float f2;
     return __builtin_bit_cast(u32, __builtin_convertvector((f2){a, b}, bf16x2));
   }
+  __device__ static inline float dot2_ones(u32 x, float acc) {  // acc + x.lo + x.hi
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x),
+                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+  }
 };
 template <> struct Mfma<true> {
   __device__ static inline f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
@@ -76,6 +82,10 @@ template <> struct Mfma<true> {
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
   __device__ static inline u32 pack(float a, float b) { return pack_f16x2(a, b); }
+  __device__ static inline float dot2_ones(u32 x, float acc) {  // acc + x.lo + x.hi
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), __builtin_bit_cast(f16x2, 0x3c003c00u),
+                                  acc, false);
+  }
 };
 
 // byte-select masks for v_perm_b32(hi_src, lo_src, sel)
@@ -100,10 +110,14 @@ __device__ __forceinline__ int vt_octet_off(int row, int g, int hl) {
   return row * BKV + (((2 * g + hl) ^ ((row ^ (row >> 3)) & 7)) * 8);
 }
 
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 template <int G, bool CAUSAL, bool F16>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
-  constexpr int HPW = 1;               // query heads per wave
-  constexpr int WH = G / HPW;          // head slots per workgroup
+  constexpr int WH = G;                // head slots per workgroup (one head per wave)
   constexpr int WQ = kWaves / WH;      // 32-query slots per workgroup
   constexpr int BQ = 32 * WQ;
   static_assert(WH * WQ == kWaves, "eight waves per workgroup");
@@ -141,65 +155,61 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   const int nsub = (w_end + 31) / 32;       // 32-key sub-tiles this wave computes
 
   // Q fragments: B operand of S^T = K Q^T, lane = query column, 8 dims.
-  u32x4 qf[HPW][8];
+  u32x4 qf[8];
   {
     const int qrow = q_beg + min(qi, max(Lq - 1, 0));  // clamped: rows >= Lq are never stored
+    const u16* qp = a.q + (int64_t)qrow * a.q_stride + (h * G + wh) * D + hl * 8;
 #pragma unroll
-    for (int j = 0; j < HPW; ++j) {
-      const u16* qp = a.q + (int64_t)qrow * a.q_stride + (h * G + wh * HPW + j) * D + hl * 8;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) qf[j][t] = *reinterpret_cast<const u32x4*>(qp + 16 * t);
-    }
+    for (int t = 0; t < 8; ++t) qf[t] = *reinterpret_cast<const u32x4*>(qp + 16 * t);
   }
 
-  f32x16 o[HPW][4];
-  float m[HPW], l[HPW];  // m: running max of the raw scores (scale applied in exp2)
+  f32x16 o[4];
 #pragma unroll
-  for (int j = 0; j < HPW; ++j) {
-    m[j] = -1e30f;
-    l[j] = 0.f;
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[j][c][i] = 0.f;
-  }
+    for (int i = 0; i < 16; ++i) o[c][i] = 0.f;
+  float m = -1e30f, l = 0.f;  // m: reference max of the raw scores (scale applied in exp2)
 
-  // Staging: waves 0-3 stage K (thread loads rows (tid>>4) + 16*i), waves
-  // 4-7 stage V (thread loads rows 4*(tid>>4) + i, transposed into V^T), 16 B
-  // at dim (tid&15)*8.  Rows past kv_end are clamped to the last visible row
-  // (finite data; those keys are masked, so p = 0 multiplies it).
+  // ---- staging.  Waves 0-3 stage K (thread: rows (tid>>4) + 16*i), waves
+  // 4-7 stage V (thread: rows 4*(tid>>4) + i, transposed into V^T), 16 B at
+  // dim (tid&15)*8.  Buffer loads return zeros for rows >= kv_end (the
+  // resource covers exactly the visible rows), so tails need no clamping.
   const bool k_role = tid < 256;
   const int st_r = (tid & 255) >> 4, st_c = (tid & 15) * 8;
-  const u16* sg = k_role ? a.k + (int64_t)k_beg * a.k_stride + h * D + st_c
-                         : a.v + (int64_t)k_beg * a.v_stride + h * D + st_c;
-  const int64_t sg_stride = k_role ? a.k_stride : a.v_stride;
-  const int last = max(kv_end - 1, 0);
+  const int64_t sg_stride = k_role ? a.k_stride : a.v_stride;  // elements
+  const u16* sg_base = (k_role ? a.k + (int64_t)k_beg * a.k_stride : a.v + (int64_t)k_beg * a.v_stride) + h * D;
+  const int row_bytes = (int)(sg_stride * 2);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u16*>(sg_base), 0, kv_end > 0 ? (kv_end - 1) * row_bytes + D * 2 : 0, 0x00020000);
+  // per-thread staging offsets: global (bytes, one VGPR; the row step goes
+  // into the scalar offset) and LDS (elements)
+  const int st_voff = (k_role ? st_r : st_r * 4) * row_bytes + st_c * 2;
+  const int st_rstep = k_role ? 16 * row_bytes : row_bytes;
+  const int k_woff = st_r * KPITCH + st_c;
   u32x4 sp[4];
 
-  // per-lane LDS read offsets (elements)
+  // per-lane LDS read offsets (elements).  For V^T row 32c + col the octet
+  // swizzle term is sw0 ^ 4*(c & 1), so the octet of key group g is
+  // (hl ^ sw0) ^ 4*(c&1) ^ 2*g: four distinct offsets cover every (c, g).
   const int k_rd = col * KPITCH + hl * 8;
-  int v_row[4], v_x[4];
+  const int v_base = col * BKV;
+  int v_oct[4];
+  {
+    const int x0 = hl ^ ((col ^ (col >> 3)) & 7);
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int row = 32 * c + col;
-    v_row[c] = row * BKV;
-    v_x[c] = hl ^ ((row ^ (row >> 3)) & 7);
+    for (int k = 0; k < 4; ++k) v_oct[k] = (x0 ^ (2 * k)) << 3;
   }
 
   auto prefetch = [&](int t) {
-    const int k0 = t * BKV;
+    const int soff = t * BKV * row_bytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = k_role ? k0 + st_r + 16 * i : k0 + st_r * 4 + i;
-      sp[i] = *reinterpret_cast<const u32x4*>(sg + (int64_t)min(r, last) * sg_stride);
-    }
+    for (int i = 0; i < 4; ++i) sp[i] = buf_load16(rs, st_voff, soff + i * st_rstep);
   };
   auto stage_write = [&](int t) {
     if (k_role) {
-      u16* ks = Ks[t % STAGES];
+      u16* ks = Ks[t % STAGES] + k_woff;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<u32x4*>(ks + (st_r + 16 * i) * KPITCH + st_c) = sp[i];
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(ks + 16 * i * KPITCH) = sp[i];
     } else {
       u16* vt = Vt[t % STAGES];
 #pragma unroll
@@ -214,95 +224,38 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
       }
     }
   };
-  // S^T for 32-key sub-tile j (keys 32j..32j+31) of every head of this wave
-  auto scores = [&](int j, f32x16* st) {
+  // S^T (scores of sub-tile j: keys 32j..32j+31) for this wave's head
+  auto scores = [&](int j) {
     const u16* kr = Ks[(j >> 1) % STAGES] + (j & 1) * 32 * KPITCH + k_rd;
+    f32x16 st;
 #pragma unroll
-    for (int x = 0; x < HPW; ++x)
+    for (int i = 0; i < 16; ++i) st[i] = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) st[x][i] = 0.f;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const u32x4 ka = *reinterpret_cast<const u32x4*>(kr + 16 * t);
-#pragma unroll
-      for (int x = 0; x < HPW; ++x) st[x] = M::run(ka, qf[x][t], st[x]);
-    }
+    for (int t = 0; t < 8; ++t) st = M::run(*reinterpret_cast<const u32x4*>(kr + 16 * t), qf[t], st);
+    return st;
   };
-  // online softmax of one sub-tile (log2 domain, raw-score running max);
-  // returns P^T as the B operand of the PV product
-  auto softmax = [&](int j, f32x16* st, u32x4 (*pb)[2], bool first) {
-    const int kb = 32 * j;
-    const bool need_mask = kb + 32 > w_full;  // wave-uniform
+
+  auto pv_step = [&](int jp, const u32x4* pb) {  // O += V(jp) P(jp)
+    const u16* vt = Vt[(jp >> 1) % STAGES] + v_base;
+    const int g0 = 2 * (jp & 1);
 #pragma unroll
-    for (int x = 0; x < HPW; ++x) {
-      if (need_mask) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kb + 8 * (i >> 2) + 4 * hl + (i & 3);
-          st[x][i] = key < my_lim ? st[x][i] : -INFINITY;
-        }
-      }
-      float mx = fmaxf(st[x][0], st[x][1]);
-#pragma unroll
-      for (int i = 2; i < 16; ++i) mx = fmaxf(mx, st[x][i]);
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
-                                                       false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      // Lazy rescaling: the reference max m only moves when some row's max
-      // exceeds it by more than kRescale (log2 units), so p <= 2^kRescale and
-      // the O/l accumulators (exactly normalised at the end) are rescaled
-      // rarely; on the first sub-tile they are still zero.
-      const float grow = (mx - m[x]) * a.scale_log2;
-      if (first) {
-        m[x] = fmaxf(mx, -1e30f);
-      } else if (__any(grow > kRescale)) {
-        const float mn = fmaxf(m[x], mx);
-        const float alpha = fast_exp2((m[x] - mn) * a.scale_log2);
-        m[x] = mn;
-        l[x] *= alpha;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[x][c][i] *= alpha;
-      }
-      const float nb = -m[x] * a.scale_log2;
-      float p[16];
-      float ps = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        p[i] = fast_exp2(fmaf(st[x][i], a.scale_log2, nb));
-        ps += p[i];
-      }
-      l[x] += ps;
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) pb[x][tt][w] = M::pack(p[8 * tt + 2 * w], p[8 * tt + 2 * w + 1]);
-    }
-  };
-  auto pv = [&](int j, u32x4 (*pb)[2]) {
-    const u16* vt = Vt[(j >> 1) % STAGES];
-    const int g0 = 2 * (j & 1);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        const u32x4 va =
-            *reinterpret_cast<const u32x4*>(vt + v_row[c] + ((v_x[c] ^ (2 * (g0 + tt))) << 3));
-#pragma unroll
-        for (int x = 0; x < HPW; ++x) o[x][c] = M::run(va, pb[x][tt], o[x][c]);
+        const int k = (2 * (c & 1)) ^ (g0 + tt);  // (4*(c&1) ^ 2*g) / 2
+        const u32x4 va = *reinterpret_cast<const u32x4*>(vt + 32 * c * BKV + v_oct[k]);
+        o[c] = M::run(va, pb[tt], o[c]);
       }
-    }
   };
 
   // Prologue: tile 0 in LDS, tile 1 in flight, S of sub-tile 0.
-  f32x16 sc[HPW];
+  f32x16 sc;
   if (nt > 0) {
     prefetch(0);
     stage_write(0);
     if (nt > 1) prefetch(1);
     __syncthreads();
-    if (nsub > 0) scores(0, sc);
+    sc = scores(0);
   }
 
   // Ring hazard: tile t+1 is written to stage (t+1)%3 after the barrier of
@@ -317,13 +270,61 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     for (int sub = 0; sub < 2; ++sub) {
       const int j = 2 * t + sub;
       if (j < nsub) {  // wave-uniform
-        f32x16 sn[HPW];
-        if (j + 1 < nsub) scores(j + 1, sn);
-        u32x4 pb[HPW][2];
-        softmax(j, sc, pb, j == 0);
-        pv(j, pb);
+        // ---- causal mask (only sub-tiles that cross this wave's diagonal)
+        const int kb = 32 * j;
+        if (kb + 32 > w_full) {
 #pragma unroll
-        for (int x = 0; x < HPW; ++x) sc[x] = sn[x];
+          for (int i = 0; i < 16; ++i) {
+            const int key = kb + 8 * (i >> 2) + 4 * hl + (i & 3);
+            sc[i] = key < my_lim ? sc[i] : -INFINITY;
+          }
+        }
+        // ---- row max (the partner lane l^32 holds the other 16 keys)
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
+#pragma unroll
+        for (int i = 3; i < 15; i += 2) mx = fmaxf(mx, fmaxf(sc[i], sc[i + 1]));
+        mx = fmaxf(mx, sc[15]);
+        {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                           false, false);
+          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        // Lazy rescaling: the reference max m only moves when some row max
+        // exceeds it by more than kRescale (log2 units), so p <= 2^kRescale
+        // and the accumulators (normalised exactly at the end) are rescaled
+        // rarely; on the first sub-tile they are still zero.
+        if (j == 0) {
+          m = fmaxf(mx, -1e30f);
+        } else if (__any((mx - m) * a.scale_log2 > kRescale)) {
+          const float mn = fmaxf(m, mx);
+          const float alpha = fast_exp2((m - mn) * a.scale_log2);
+          m = mn;
+          l *= alpha;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[c][i] *= alpha;
+        }
+        // ---- look-ahead scores of sub-tile j+1 (MFMA) beside the
+        // exponentials of sub-tile j (VALU).  Past the wave's last sub-tile
+        // the look-ahead reads a stale stage and its result is discarded.
+        const float nb = -m * a.scale_log2;
+        const f32x16 sn = scores(j + 1);
+        float p[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sc[i], a.scale_log2, nb));
+        u32x4 pb[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) pb[tt][w] = M::pack(p[8 * tt + 2 * w], p[8 * tt + 2 * w + 1]);
+        // row sum of the rounded probabilities the PV product uses
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) l = M::dot2_ones(pb[tt][w], l);
+        pv_step(j, pb);
+        sc = sn;
       }
     }
   }
@@ -331,22 +332,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   // ---- epilogue: full row sum (partner lane holds the other 16 keys of each
   // 32-key sub-tile), normalise, store.
   if (!q_ok) return;
+  const float lt = l + __shfl_xor(l, 32);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  u16* op = a.out + (int64_t)(q_beg + qi) * a.o_stride + (h * G + wh) * D + 4 * hl;
 #pragma unroll
-  for (int j = 0; j < HPW; ++j) {
-    const float lt = l[j] + __shfl_xor(l[j], 32);
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    const int hq = h * G + wh * HPW + j;
-    u16* op = a.out + (int64_t)(q_beg + qi) * a.o_stride + hq * D + 4 * hl;
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        u32x2 w;
-        w[0] = M::pack(o[j][c][4 * r] * inv, o[j][c][4 * r + 1] * inv);
-        w[1] = M::pack(o[j][c][4 * r + 2] * inv, o[j][c][4 * r + 3] * inv);
-        *reinterpret_cast<u32x2*>(op + 32 * c + 8 * r) = w;
-      }
-  }
+    for (int r = 0; r < 4; ++r) {
+      u32x2 w;
+      w[0] = M::pack(o[c][4 * r] * inv, o[c][4 * r + 1] * inv);
+      w[1] = M::pack(o[c][4 * r + 2] * inv, o[c][4 * r + 3] * inv);
+      *reinterpret_cast<u32x2*>(op + 32 * c + 8 * r) = w;
+    }
 }
 
 template <int G, bool CAUSAL, bool F16>
@@ -394,6 +391,9 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) % 16 || q_tok_stride % 8 ||
       k_tok_stride % 8 || v_tok_stride % 8 || out_tok_stride % 8)
     return AAC_ERR_MISALIGNED;
+  // staging uses 32-bit byte offsets within one segment's K/V rows
+  if ((int64_t)max_seqlen_k * std::max(k_tok_stride, v_tok_stride) * 2 >= (int64_t(1) << 31))
+    return AAC_ERR_UNSUPPORTED;
   if (!launch) return AAC_OK;
   pf::Args a;
   a.q = (const u16*)q;
