@@ -83,18 +83,23 @@ def _token_rows(t: torch.Tensor, name: str) -> int:
 # ---------------------------------------------------------------- workspace
 _ws_lock = threading.Lock()
 _ws: dict[int, torch.Tensor] = {}
+_ws_retired: list[torch.Tensor] = []
 
 
 def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     """Per-device scratch for split-K partials, grown on demand.
 
-    Calls that overlap on different streams of one device would share it;
-    the reference issues every attention call from one thread on one stream.
+    A buffer that is outgrown is kept alive rather than freed: a captured
+    HIP graph may hold its address.  Calls that overlap on different streams
+    of one device would share it; the reference issues every attention call
+    from one thread on one stream.
     """
     idx = device.index if device.index is not None else torch.cuda.current_device()
     with _ws_lock:
         buf = _ws.get(idx)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                _ws_retired.append(buf)
             buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             _ws[idx] = buf
         return buf

@@ -1,0 +1,315 @@
+"""Continuous-batching Qwen3 engine on the gfx950 attention kernels.
+
+Restates the reference's single-GPU engine (llm.py:36-446): an async request
+queue served by a background loop that, each iteration, (1) drains the queue,
+(2) admits waiting prompts while capacity lasts, (3) runs one packed varlen
+prefill for the newly admitted prompts and samples their first token, (4)
+runs one batched decode step for every active sequence, and (5) retires
+finished sequences.  Finish rule (llm.py:371, :421-425): ``len(tokens) >=
+max_tokens``, position ``>= max_seq_len``, or EOS unless ``ignore_eos``.
+Greedy sampling at temperature 0 (llm.py:215-219).
+
+Changes on the hot path:
+
+* Capacity is a pool of fixed-size KV blocks (``BlockAllocator``) instead of
+  one ``max_seq_len`` slot per sequence; a sequence is admitted when a batch
+  row and the blocks for ``min(prompt + max_tokens, max_seq_len)`` tokens are
+  free (so it can never run out of cache mid-generation).
+* Per-step metadata (token ids, positions, cache lengths, block tables) is
+  packed on the host and copied to the device once per step; the model has no
+  per-layer host synchronisation (the reference syncs in RoPE,
+  model/model.py:82, and writes decode inputs element by element,
+  llm.py:395-398).
+* No tokenizer is available offline, so prompts are token-id lists and
+  ``GenerationOutput.text`` is empty unless a ``decode_fn`` is supplied.
+"""
+from __future__ import annotations
+
+import bisect
+import concurrent.futures
+import math
+import queue
+import threading
+import time
+from dataclasses import dataclass, field
+from typing import Callable, Optional
+
+import numpy as np
+import torch
+
+from .paged import BlockAllocator, build_prefill_metadata, pad_block_tables
+from .qwen3 import PagedKVCache, Qwen3Config, Qwen3ForCausalLM, StepMeta
+
+__all__ = ["LLM", "GenerationOutput"]
+
+
+@dataclass
+class GenerationOutput:
+    """Result of one prompt (llm.py:15-21)."""
+    text: str
+    token_ids: list[int]
+    prompt_tokens: int = 0
+    generated_tokens: int = 0
+
+
+@dataclass
+class _Request:
+    """Internal request record (llm.py:24-33)."""
+    token_ids: list[list[int]]
+    max_tokens: int
+    temperature: float
+    ignore_eos: bool
+    future: concurrent.futures.Future
+    results: list = field(default_factory=list)
+    pending_indices: list = field(default_factory=list)
+
+
+@dataclass
+class _Seq:
+    req: _Request
+    prompt_idx: int
+    row: int                 # batch row (the reference's slot id)
+    blocks: list[int]
+    tokens: list[int]        # generated so far
+    pos: int                 # position of the next token to feed
+
+
+class LLM:
+    """Qwen3 engine with continuous batching and a paged KV cache.
+
+    ``max_num_seqs`` bounds the decode batch (the reference's slot count);
+    ``num_blocks`` defaults to enough blocks for ``max_num_seqs`` sequences
+    of ``max_seq_len`` tokens.
+    """
+
+    def __init__(self, config: Optional[Qwen3Config] = None, max_num_seqs: int = 32,
+                 max_seq_len: int = 4096, dtype=torch.bfloat16, block_size: int = 256,
+                 num_blocks: Optional[int] = None, seed: int = 0, device="cuda",
+                 decode_fn: Optional[Callable[[list[int]], str]] = None, use_graphs: bool = True):
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.config = config or Qwen3Config()
+        self.max_seq_len = max_seq_len
+        self.max_num_seqs = max_num_seqs
+        self.block_size = block_size
+        self.blocks_per_seq = math.ceil(max_seq_len / block_size)
+        if num_blocks is None:
+            num_blocks = max_num_seqs * self.blocks_per_seq
+        self.decode_fn = decode_fn
+        self.model = Qwen3ForCausalLM(self.config, self.device, dtype, seed)
+        # block 0 is a scratch block: padding rows of a graph-captured decode
+        # step append into it, so they never touch a live sequence's cache
+        self.cache = PagedKVCache(self.config, num_blocks + 1, block_size, self.device, dtype)
+        self.allocator = BlockAllocator(num_blocks + 1)
+        self.allocator.allocate(1)
+        self.use_graphs = use_graphs
+        self._graphs: dict[int, tuple] = {}
+        # packed per-step host metadata: ids | positions | seqlens | tables
+        W = self.blocks_per_seq
+        self._host = torch.zeros(max_num_seqs * (3 + W), dtype=torch.int32, pin_memory=True)
+        self._dev = torch.zeros(max_num_seqs * (3 + W), dtype=torch.int32, device=self.device)
+        self._request_queue: queue.Queue[_Request] = queue.Queue()
+        self._loop_running = False
+        self._loop_thread: Optional[threading.Thread] = None
+        self.stats = dict(prefill_calls=0, decode_steps=0, prefill_tokens=0, decode_tokens=0)
+
+    # ------------------------------------------------------------------ API
+    def generate(self, prompts: list[list[int]], max_tokens: int = 100, temperature: float = 0.0,
+                 ignore_eos: bool = False) -> concurrent.futures.Future:
+        """Submit token-id prompts; the future resolves to ``list[GenerationOutput]``
+        in prompt order (llm.py:225-264)."""
+        if not prompts:
+            raise ValueError("no prompts")
+        for p in prompts:
+            if not p:
+                raise ValueError("empty prompt")
+            if len(p) >= self.max_seq_len:
+                raise ValueError(f"prompt of {len(p)} tokens does not fit max_seq_len "
+                                 f"{self.max_seq_len}")
+        self._ensure_loop()
+        fut: concurrent.futures.Future = concurrent.futures.Future()
+        req = _Request(token_ids=[list(map(int, p)) for p in prompts], max_tokens=max_tokens,
+                       temperature=temperature, ignore_eos=ignore_eos, future=fut,
+                       results=[None] * len(prompts), pending_indices=list(range(len(prompts))))
+        self._request_queue.put(req)
+        return fut
+
+    def stop(self, timeout: float = 30.0):
+        """Stop the background loop (llm.py:302-309)."""
+        if not self._loop_running:
+            return
+        self._loop_running = False
+        if self._loop_thread:
+            self._loop_thread.join(timeout=timeout)
+            self._loop_thread = None
+
+    def _ensure_loop(self):
+        if not self._loop_running:
+            self._loop_running = True
+            self._loop_thread = threading.Thread(target=self._inference_loop, daemon=True)
+            self._loop_thread.start()
+
+    # ------------------------------------------------------------ core steps
+    def _sample(self, logits: torch.Tensor, temperature: float) -> list[int]:
+        if temperature == 0:
+            return logits.argmax(dim=-1).tolist()
+        probs = torch.softmax(logits.float() / temperature, dim=-1)
+        return torch.multinomial(probs, 1).squeeze(-1).tolist()
+
+    def _prefill(self, seqs: list[_Seq]) -> torch.Tensor:
+        """Packed varlen prefill of newly admitted sequences (llm.py:116-208)."""
+        prompts = [s.req.token_ids[s.prompt_idx] for s in seqs]
+        lens = [len(p) for p in prompts]
+        tables = pad_block_tables([s.blocks for s in seqs], self.blocks_per_seq)
+        cu, positions, slots = build_prefill_metadata(lens, tables, self.block_size, self.device)
+        ids = torch.from_numpy(np.fromiter((t for p in prompts for t in p), dtype=np.int64,
+                                           count=sum(lens))).to(self.device)
+        last = (cu[1:] - 1).long()
+        meta = StepMeta(positions=positions, cu_seqlens=cu, slot_mapping=slots,
+                        max_seqlen=max(lens), last_idx=last)
+        self.stats["prefill_calls"] += 1
+        self.stats["prefill_tokens"] += sum(lens)
+        return self.model.forward(ids, meta, self.cache, prefill=True)
+
+    def _decode_meta(self, B: int, max_context_len: int) -> StepMeta:
+        d, W = self._dev, self.blocks_per_seq
+        return StepMeta(positions=d[B:2 * B], cache_seqlens=d[2 * B:3 * B],
+                        block_tables=d[3 * B:3 * B + B * W].view(B, W),
+                        max_context_len=max_context_len)
+
+    def _decode_step(self, seqs: list[_Seq]) -> torch.Tensor:
+        """One token for every active sequence (llm.py:210-213, model/model.py:233-241).
+
+        With graphs enabled the batch is padded to a power-of-two bucket and
+        the captured step of that bucket is replayed; padding rows append to
+        the scratch block 0 at position 0 and their logits are dropped.
+        """
+        n, W = len(seqs), self.blocks_per_seq
+        B = min(1 << (n - 1).bit_length(), self.max_num_seqs) if self.use_graphs else n
+        h = self._host.numpy()
+        h[:3 * B + B * W] = 0
+        h[:n] = [s.tokens[-1] for s in seqs]
+        h[B:B + n] = [s.pos for s in seqs]
+        h[2 * B:2 * B + n] = [s.pos for s in seqs]  # tokens already in the cache
+        tab = h[3 * B:3 * B + B * W].reshape(B, W)
+        for i, s in enumerate(seqs):
+            tab[i, :len(s.blocks)] = s.blocks
+        m = B * (3 + W)
+        self._dev[:m].copy_(self._host[:m], non_blocking=True)
+        self.stats["decode_steps"] += 1
+        self.stats["decode_tokens"] += n
+        if not self.use_graphs:
+            meta = self._decode_meta(B, self.blocks_per_seq * self.block_size)
+            return self.model.forward(self._dev[:B], meta, self.cache, prefill=False)
+        g = self._graphs.get(B)
+        if g is None:
+            g = self._capture(B)
+        g[0].replay()
+        return g[1][:n]
+
+    def _capture(self, B: int):
+        """Capture one decode step of batch B as a HIP graph.  Every launch
+        reads its inputs from the static metadata buffer; the attention grid
+        is sized by the block-table capacity, so the graph is valid for every
+        step of this bucket."""
+        meta = self._decode_meta(B, self.blocks_per_seq * self.block_size)
+        ids = self._dev[:B]
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            for _ in range(2):  # warm up: workspace and allocator pools
+                self.model.forward(ids, meta, self.cache, prefill=False)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits = self.model.forward(ids, meta, self.cache, prefill=False)
+        self._graphs[B] = (graph, logits)
+        return self._graphs[B]
+
+    # ------------------------------------------------------------ the loop
+    def _finish(self, s: _Seq, free_rows: list[int]):
+        req = s.req
+        text = self.decode_fn(s.tokens) if self.decode_fn else ""
+        req.results[s.prompt_idx] = GenerationOutput(
+            text, list(s.tokens), len(req.token_ids[s.prompt_idx]), len(s.tokens))
+        self.allocator.free(s.blocks)
+        bisect.insort(free_rows, s.row)
+        if all(r is not None for r in req.results):
+            req.future.set_result(req.results)
+
+    def _should_stop(self, s: _Seq, tok: int) -> bool:
+        return (len(s.tokens) >= s.req.max_tokens or s.pos >= self.max_seq_len
+                or (not s.req.ignore_eos and tok == self.config.eos_token_id))
+
+    @torch.inference_mode()
+    def _inference_loop(self):
+        free_rows = list(range(self.max_num_seqs))
+        active: dict[int, _Seq] = {}
+        pending: list[_Request] = []
+        try:
+            while self._loop_running or pending or active:
+                # Phase 1: drain the queue
+                while True:
+                    try:
+                        pending.append(self._request_queue.get_nowait())
+                    except queue.Empty:
+                        break
+                if not pending and not active:
+                    if not self._loop_running:
+                        break
+                    time.sleep(0.001)
+                    continue
+                # Phase 2: admit while a batch row and the blocks are free
+                new: list[_Seq] = []
+                for req in list(pending):
+                    while req.pending_indices and free_rows:
+                        pi = req.pending_indices[0]
+                        L = len(req.token_ids[pi])
+                        need = math.ceil(min(L + req.max_tokens, self.max_seq_len) / self.block_size)
+                        if need > self.allocator.num_free:
+                            break
+                        req.pending_indices.pop(0)
+                        new.append(_Seq(req, pi, free_rows.pop(0), self.allocator.allocate(need),
+                                        [], L))
+                    if not req.pending_indices:
+                        pending.remove(req)
+                    elif not free_rows or self.allocator.num_free == 0:
+                        break
+                # Phase 3: prefill the admitted prompts, sample their first token
+                if new:
+                    sampled = self._sample(self._prefill(new), new[0].req.temperature)
+                    for s, tok in zip(new, sampled):
+                        s.tokens.append(tok)
+                        if 1 >= s.req.max_tokens or (not s.req.ignore_eos
+                                                     and tok == self.config.eos_token_id):
+                            self._finish(s, free_rows)
+                        else:
+                            active[s.row] = s
+                if not active:
+                    continue
+                # Phase 4: one decode step for every active sequence
+                seqs = [active[r] for r in sorted(active)]
+                sampled = self._sample(self._decode_step(seqs), seqs[0].req.temperature)
+                # Phase 5: bookkeeping
+                for s, tok in zip(seqs, sampled):
+                    s.tokens.append(tok)
+                    s.pos += 1
+                    if self._should_stop(s, tok):
+                        del active[s.row]
+                        self._finish(s, free_rows)
+        except BaseException as e:  # surface failures to every waiting caller
+            for s in active.values():
+                if not s.req.future.done():
+                    s.req.future.set_exception(e)
+            for req in pending:
+                if not req.future.done():
+                    req.future.set_exception(e)
+            while True:
+                try:
+                    req = self._request_queue.get_nowait()
+                except queue.Empty:
+                    break
+                if not req.future.done():
+                    req.future.set_exception(e)
+            self._loop_running = False
+            raise

@@ -1,0 +1,236 @@
+"""Qwen3 decoder whose attention runs on the gfx950 kernels.
+
+Mirrors the reference's single-GPU model (model/model.py): fused QKV
+projection (model/model.py:132-154), per-head q/k RMSNorm
+(model/model.py:40-52, :225-226), RoPE applied in the activation dtype
+(model/model.py:55-99, :228), and the attention call site
+(TransformerBlock.forward, model/model.py:202-267).  Differences, all on the
+hot path:
+
+* The KV cache is paged: per layer one K and one V tensor of shape
+  ``[num_blocks, block_size, Hkv, D]`` (model/model.py:324-336 keeps one
+  ``max_seq_len`` slot per sequence -- the special case of one block per
+  sequence).
+* Prefill stores K/V through ``slot_mapping`` and runs causal varlen
+  attention in one library call (llm.py:171-184); decode appends the new K/V
+  at ``cache_seqlens`` and attends (model/model.py:233-240).  The caller keeps
+  ``cache_seqlens`` (model/model.py:241 increments it after the call).
+* RoPE cos/sin come from a table precomputed for ``max_position`` tokens, so
+  no per-layer ``position_ids.max().item()`` host sync (model/model.py:82).
+
+Weights are random-initialised (no checkpoint is available offline);
+``init_weights`` draws them from N(0, 0.02) with RMSNorm weights at 1, which
+keeps activations finite through all layers.
+"""
+from __future__ import annotations
+
+import json
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import flash_attn_interface as fai
+
+__all__ = ["Qwen3Config", "Qwen3ForCausalLM", "PagedKVCache", "StepMeta"]
+
+
+@dataclass
+class Qwen3Config:
+    """Same fields and defaults as the reference's Qwen3Config (model/model.py:13-37)."""
+    vocab_size: int = 151936
+    hidden_size: int = 1024
+    intermediate_size: int = 3072
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    max_position_embeddings: int = 40960
+    rope_theta: float = 1000000.0
+    rms_norm_eps: float = 1e-6
+    hidden_act: str = "silu"
+    tie_word_embeddings: bool = True
+    bos_token_id: int = 151643
+    eos_token_id: int = 151645
+
+    @classmethod
+    def from_json(cls, path: str):
+        with open(path) as f:
+            data = json.load(f)
+        return cls(**{k: v for k, v in data.items() if k in cls.__annotations__})
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm with the reference's numerics (model/model.py:47-52): statistics
+    in fp32, normalised value cast back to the input dtype, then scaled."""
+    dt = x.dtype
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * xf.to(dt)
+
+
+class Rope:
+    """cos/sin tables in the activation dtype (model/model.py:64-78), indexed
+    by position on the device."""
+
+    def __init__(self, head_dim: int, max_pos: int, theta: float, device, dtype):
+        inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+        t = torch.arange(max_pos, dtype=torch.float32)
+        freqs = torch.outer(t, inv)
+        emb = torch.cat((freqs, freqs), dim=-1)
+        self.cos = emb.cos().to(device=device, dtype=dtype)
+        self.sin = emb.sin().to(device=device, dtype=dtype)
+        self.half = head_dim // 2
+
+    def apply(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """x [T, H, D], positions [T] -> x*cos + rotate_half(x)*sin (model/model.py:86-99)."""
+        cos = self.cos[positions].unsqueeze(1)
+        sin = self.sin[positions].unsqueeze(1)
+        x1, x2 = x[..., :self.half], x[..., self.half:]
+        rot = torch.cat((-x2, x1), dim=-1)
+        return x * cos + rot * sin
+
+
+class PagedKVCache:
+    """Per-layer paged K/V caches ``[num_blocks, block_size, Hkv, D]``,
+    zero-initialised like model/model.py:328-335."""
+
+    def __init__(self, cfg: Qwen3Config, num_blocks: int, block_size: int, device, dtype):
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        shape = (cfg.num_hidden_layers, 2, num_blocks, block_size, cfg.num_key_value_heads,
+                 cfg.head_dim)
+        self.storage = torch.zeros(shape, device=device, dtype=dtype)
+
+    def k(self, layer: int) -> torch.Tensor:
+        return self.storage[layer, 0]
+
+    def v(self, layer: int) -> torch.Tensor:
+        return self.storage[layer, 1]
+
+    @property
+    def nbytes(self) -> int:
+        return self.storage.numel() * self.storage.element_size()
+
+
+@dataclass
+class StepMeta:
+    """Device-side metadata of one forward pass.
+
+    prefill: ``cu_seqlens`` int32 [n+1], ``positions`` int64 [N],
+             ``slot_mapping`` int64 [N], ``max_seqlen``, ``last_idx`` int64 [n]
+    decode:  ``positions`` int64 [B], ``block_tables`` int32 [B, W],
+             ``cache_seqlens`` int32 [B] (length before this step's append),
+             ``max_context_len`` (upper bound on cache_seqlens + 1)
+    """
+    positions: torch.Tensor
+    cu_seqlens: torch.Tensor | None = None
+    slot_mapping: torch.Tensor | None = None
+    max_seqlen: int = 0
+    last_idx: torch.Tensor | None = None
+    block_tables: torch.Tensor | None = None
+    cache_seqlens: torch.Tensor | None = None
+    max_context_len: int = 0
+
+
+class Qwen3ForCausalLM:
+    """Random-initialised Qwen3 with tied embeddings (model/model.py:289-322)."""
+
+    def __init__(self, cfg: Qwen3Config, device, dtype=torch.bfloat16, seed: int = 0):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.hq, self.hkv, self.d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.q_size = self.hq * self.d
+        self.kv_size = self.hkv * self.d
+        self.scale = self.d ** -0.5
+        self.init_weights(seed)
+        self.rope = Rope(self.d, cfg.max_position_embeddings, cfg.rope_theta, self.device, dtype)
+
+    @torch.no_grad()
+    def init_weights(self, seed: int, std: float = 0.02):
+        cfg, dev, dt = self.cfg, self.device, self.dtype
+        g = torch.Generator(device=dev).manual_seed(seed)
+
+        def rnd(*shape):
+            return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std).to(dt)
+
+        H, I = cfg.hidden_size, cfg.intermediate_size
+        self.embed = rnd(cfg.vocab_size, H)
+        self.layers = []
+        for _ in range(cfg.num_hidden_layers):
+            self.layers.append(dict(
+                ln1=torch.ones(H, device=dev, dtype=dt),
+                ln2=torch.ones(H, device=dev, dtype=dt),
+                q_norm=torch.ones(self.d, device=dev, dtype=dt),
+                k_norm=torch.ones(self.d, device=dev, dtype=dt),
+                qkv=rnd(self.q_size + 2 * self.kv_size, H),   # fused [Q | K | V]
+                o=rnd(H, self.q_size),
+                gate_up=rnd(2 * I, H),                         # fused [gate | up]
+                down=rnd(H, I),
+            ))
+        self.norm = torch.ones(H, device=dev, dtype=dt)
+
+    # ---------------------------------------------------------------- layers
+    def _qkv(self, L, h, positions):
+        """Fused QKV, q/k RMSNorm, RoPE.  Returns q [T,Hq,D], k [T,Hkv,D] (new
+        tensors) and v [T,Hkv,D] (a strided view of the qkv buffer, as at
+        llm.py:156)."""
+        T = h.shape[0]
+        eps = self.cfg.rms_norm_eps
+        qkv = F.linear(h, L["qkv"])
+        q = qkv[:, :self.q_size].view(T, self.hq, self.d)
+        k = qkv[:, self.q_size:self.q_size + self.kv_size].view(T, self.hkv, self.d)
+        v = qkv[:, self.q_size + self.kv_size:].view(T, self.hkv, self.d)
+        q = rms_norm(q, L["q_norm"], eps)
+        k = rms_norm(k, L["k_norm"], eps)
+        q = self.rope.apply(q, positions)
+        k = self.rope.apply(k, positions)
+        return q, k, v
+
+    def _mlp(self, L, h):
+        gu = F.linear(h, L["gate_up"])
+        I = self.cfg.intermediate_size
+        return F.linear(F.silu(gu[:, :I]) * gu[:, I:], L["down"])
+
+    def _layer(self, li, h, meta: StepMeta, cache: PagedKVCache, prefill: bool):
+        L = self.layers[li]
+        eps = self.cfg.rms_norm_eps
+        res = h
+        x = rms_norm(h, L["ln1"], eps)
+        q, k, v = self._qkv(L, x, meta.positions)
+        if prefill:
+            # store K/V through slot_mapping and attend (llm.py:171-184)
+            attn = fai.varlen_prefill_with_kvcache(
+                q, k, v, meta.cu_seqlens, meta.max_seqlen, cache.k(li), cache.v(li),
+                meta.slot_mapping, softmax_scale=self.scale, causal=True)
+        else:
+            # append at cache_seqlens and attend (model/model.py:233-240)
+            B = q.shape[0]
+            attn = fai.flash_attn_with_kvcache(
+                q.view(B, 1, self.hq, self.d), cache.k(li), cache.v(li),
+                k=k.view(B, 1, self.hkv, self.d), v=v.view(B, 1, self.hkv, self.d),
+                cache_seqlens=meta.cache_seqlens, block_table=meta.block_tables,
+                softmax_scale=self.scale, causal=False, max_context_len=meta.max_context_len)
+        h = res + F.linear(attn.reshape(q.shape[0], -1), L["o"])
+        res = h
+        h = res + self._mlp(L, rms_norm(h, L["ln2"], eps))
+        return h
+
+    @torch.no_grad()
+    def forward(self, input_ids: torch.Tensor, meta: StepMeta, cache: PagedKVCache,
+                prefill: bool) -> torch.Tensor:
+        """Logits for the last token of every sequence: prefill takes packed
+        tokens (llm.py:116-208), decode one token per sequence
+        (model/model.py:302-322)."""
+        h = F.embedding(input_ids, self.embed)
+        for li in range(self.cfg.num_hidden_layers):
+            h = self._layer(li, h, meta, cache, prefill)
+        if prefill:
+            h = h[meta.last_idx]
+        h = rms_norm(h, self.norm, self.cfg.rms_norm_eps)
+        return F.linear(h, self.embed)  # tied embeddings
+
+    def kv_bytes_per_token(self) -> int:
+        return 2 * self.hkv * self.d * 2 * self.cfg.num_hidden_layers

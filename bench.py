@@ -16,6 +16,11 @@ Also reported on the same line:
   prefill       varlen causal prefill, 8 x 1024 tokens, 16/8 heads, bf16, with
                 the paged store in the same call, as TFLOP/s against the
                 2.5 PFLOP/s dense bf16 MFMA peak (roofline of that kernel);
+  e2e           random-init Qwen3-0.6B, 256 requests x 1024 input / 1024
+                output tokens under the continuous-batching engine: output
+                tok/s (generated tokens / wall clock from submit to the last
+                token) and total tok/s (prompt + generated), as
+                benchmark_tp.py:93-99 defines them;
   cpu_baseline  the numpy oracle on a bounded sample of the decode workload,
                 single-threaded on the host cores.
 
@@ -45,7 +50,11 @@ def parse():
     p.add_argument("--partition", type=int, default=0, help="decode partition tokens (0=auto)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true")
-    p.add_argument("--only", choices=["decode", "prefill"], default=None,
+    p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine leg")
+    p.add_argument("--e2e-seqs", type=int, default=256)
+    p.add_argument("--e2e-in", type=int, default=1024)
+    p.add_argument("--e2e-out", type=int, default=1024)
+    p.add_argument("--only", choices=["decode", "prefill", "e2e"], default=None,
                    help="run one leg only (for profiling)")
     return p.parse_args()
 
@@ -173,6 +182,41 @@ def bench_prefill(torch, fai, paged, dev, args):
 
 
 # ----------------------------------------------------------------------------
+# end to end: random-init Qwen3-0.6B under the continuous-batching engine
+# ----------------------------------------------------------------------------
+def bench_e2e(torch, args):
+    from awesome_acceleration_amd.llm import LLM
+    from awesome_acceleration_amd.qwen3 import Qwen3Config
+
+    B, Lin, Lout = args.e2e_seqs, args.e2e_in, args.e2e_out
+    t0 = time.perf_counter()
+    llm = LLM(Qwen3Config(), max_num_seqs=B, max_seq_len=Lin + Lout + 16, block_size=256,
+              seed=args.seed)
+    rs = np.random.RandomState(args.seed)
+    prompts = [rs.randint(0, llm.config.vocab_size, Lin).tolist() for _ in range(B)]
+    # warm-up request (benchmark_tp.py:357-358) also captures the decode graph of
+    # the largest bucket so capture time stays out of the timed region
+    llm.generate([prompts[0][:16]] * B, max_tokens=3, ignore_eos=True).result()
+    torch.cuda.synchronize()
+    t_init = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    outs = llm.generate(prompts, max_tokens=Lout, ignore_eos=True).result()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    llm.stop()
+    gen = sum(o.generated_tokens for o in outs)
+    prompt = sum(o.prompt_tokens for o in outs)
+    return dict(
+        workload=f"Qwen3-0.6B (28 layers, hidden 1024, 16/8 heads, head_dim 128, vocab 151936, "
+                 f"random bf16 weights), {B} requests x {Lin} random input tokens, {Lout} greedy "
+                 f"output tokens each (ignore_eos), continuous-batching engine, KV block 256",
+        output_tok_s=round(gen / el, 1), total_tok_s=round((gen + prompt) / el, 1),
+        seconds=round(el, 3), generated_tokens=gen, prompt_tokens=prompt,
+        decode_steps=llm.stats["decode_steps"], setup_seconds=round(t_init, 2),
+        kv_cache_gib=round(llm.cache.nbytes / 2 ** 30, 1))
+
+
+# ----------------------------------------------------------------------------
 # CPU baseline: the oracle on a bounded sample of the decode workload
 # ----------------------------------------------------------------------------
 def cpu_baseline(x, reps=3, seed=1):
@@ -234,6 +278,8 @@ def main():
         res["decode"] = bench_decode(torch, fai, dev, args)
     if args.only in (None, "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, fai, paged, dev, args)
+    if args.only in (None, "e2e") and not args.no_e2e:
+        res["e2e"] = bench_e2e(torch, args)
     if args.only is not None:
         print(json.dumps({k: {kk: vv for kk, vv in v.items() if kk != "x"}
                           for k, v in res.items()}, default=float))
@@ -282,6 +328,8 @@ def main():
                          "frac": round(pf["tflops"] / BF16_PEAK_TFLOPS, 4),
                          "flops_per_launch": pf["flops"], "traffic": None},
         }
+    if "e2e" in res:
+        line["e2e"] = res["e2e"]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(dec["x"])
     print(json.dumps(line))

@@ -1,0 +1,112 @@
+"""The continuous-batching engine on the HIP kernels against an independent
+fp32 torch forward of the same random Qwen3 weights (teacher-forced over the
+prompt plus the generated tokens, attention by torch SDPA with causal mask and
+repeat-interleaved KV heads -- the textbook Qwen3 layer of model/model.py).
+
+Each generated token must be the reference argmax wherever the reference's
+top-2 logit margin exceeds the bf16 noise floor; graph-captured decode steps
+must reproduce the eager engine token for token."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from awesome_acceleration_amd.llm import LLM
+from awesome_acceleration_amd.qwen3 import Qwen3Config
+
+pytestmark = pytest.mark.gpu
+
+CFG = Qwen3Config(vocab_size=2048, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                  num_attention_heads=4, num_key_value_heads=2, head_dim=128,
+                  max_position_embeddings=4096)
+
+
+def reference_logits(model, ids):
+    """fp32 forward over one full sequence; returns logits [T, vocab]."""
+    cfg = model.cfg
+    dev = model.device
+    T = len(ids)
+    f = lambda t: t.float()  # noqa: E731
+    eps = cfg.rms_norm_eps
+
+    def norm(x, w):
+        return f(w) * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+
+    pos = torch.arange(T, device=dev)
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, 128, 2, device=dev).float() / 128))
+    fr = torch.outer(pos.float(), inv)
+    emb = torch.cat((fr, fr), -1)
+    cos, sin = emb.cos()[:, None], emb.sin()[:, None]
+
+    def rope(x):
+        return x * cos + torch.cat((-x[..., 64:], x[..., :64]), -1) * sin
+
+    h = f(model.embed)[torch.tensor(ids, device=dev)]
+    hq, hkv, d = model.hq, model.hkv, model.d
+    for L in model.layers:
+        x = norm(h, L["ln1"])
+        qkv = x @ f(L["qkv"]).T
+        q = qkv[:, :hq * d].view(T, hq, d)
+        k = qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
+        v = qkv[:, (hq + hkv) * d:].view(T, hkv, d)
+        q, k = rope(norm(q, L["q_norm"])), rope(norm(k, L["k_norm"]))
+        g = hq // hkv
+        a = F.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1).repeat_interleave(g, 0),
+                                           v.transpose(0, 1).repeat_interleave(g, 0), is_causal=True)
+        h = h + a.transpose(0, 1).reshape(T, -1) @ f(L["o"]).T
+        x = norm(h, L["ln2"])
+        gu = x @ f(L["gate_up"]).T
+        I = cfg.intermediate_size
+        h = h + (F.silu(gu[:, :I]) * gu[:, I:]) @ f(L["down"]).T
+    return norm(h, model.norm) @ f(model.embed).T
+
+
+def _prompts(n, seed):
+    rs = np.random.RandomState(seed)
+    return [rs.randint(0, CFG.vocab_size, rs.randint(1, 300)).tolist() for _ in range(n)]
+
+
+def _run(use_graphs, prompts, max_tokens, max_num_seqs=4):
+    llm = LLM(CFG, max_num_seqs=max_num_seqs, max_seq_len=512, block_size=64, seed=0,
+              use_graphs=use_graphs)
+    futs = [llm.generate([p], max_tokens=mt, ignore_eos=True) for p, mt in zip(prompts, max_tokens)]
+    outs = [f.result(timeout=120)[0] for f in futs]
+    llm.stop()
+    return llm, outs
+
+
+def test_engine_tokens_match_reference_and_graphs_match_eager(gpu):
+    print("case: engine continuous batching vs fp32 reference", flush=True)
+    prompts = _prompts(9, 0)
+    max_tokens = [1, 5, 12, 3, 20, 8, 2, 15, 6]
+    llm, eager = _run(False, prompts, max_tokens)
+    assert [o.generated_tokens for o in eager] == max_tokens
+    assert all(o.prompt_tokens == len(p) for o, p in zip(eager, prompts))
+    checked = 0
+    for p, o in zip(prompts, eager):
+        seq = p + o.token_ids[:-1]
+        ref = reference_logits(llm.model, seq)[len(p) - 1:]
+        top2 = ref.topk(2, dim=-1)
+        margin = (top2.values[:, 0] - top2.values[:, 1])
+        for i, tok in enumerate(o.token_ids):
+            if margin[i] > 0.05:
+                assert tok == int(top2.indices[i, 0]), f"token {i} of prompt len {len(p)}"
+                checked += 1
+    assert checked >= 0.5 * sum(max_tokens), checked
+    print(f"checked {checked} tokens against the reference", flush=True)
+    # graph-captured decode (power-of-two buckets, padding rows) == eager
+    _, graphed = _run(True, prompts, max_tokens)
+    assert [o.token_ids for o in graphed] == [o.token_ids for o in eager]
+
+
+def test_engine_admission_waits_for_blocks(gpu):
+    # a pool that holds two sequences at a time: later prompts wait for blocks
+    print("case: engine block-pool admission", flush=True)
+    llm = LLM(CFG, max_num_seqs=8, max_seq_len=256, block_size=64, num_blocks=4, seed=1)
+    prompts = [[5] * 60, [6] * 70, [7] * 10, [8] * 100]
+    outs = llm.generate(prompts, max_tokens=40, ignore_eos=True).result(timeout=120)
+    llm.stop()
+    assert [o.generated_tokens for o in outs] == [40] * 4
+    assert llm.allocator.num_free == 4  # every block returned (scratch block excluded)
+    with pytest.raises(ValueError):
+        llm.generate([[1] * 256])
