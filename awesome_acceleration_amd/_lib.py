@@ -54,6 +54,13 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _i32, _i32, _i32, _i32,
          _i32, _f32, _p, _i64, _p, _size, _i32, _i32, _p],
     ),
+    "aac_rmsnorm": (_c_int, [_p, _i64, _p, _p, _p, _p, _i64, _i32, _f32, _i32, _p]),
+    "aac_qk_norm_rope_store": (
+        _c_int,
+        [_p, _i64, _i64, _i32, _i32, _i32, _p, _p, _f32, _p, _p, _i32, _p, _p, _p, _p, _p, _i64,
+         _p, _p, _i32, _p, _i32, _i32, _p],
+    ),
+    "aac_silu_mul": (_c_int, [_p, _p, _i64, _i32, _i32, _p]),
 }
 
 ABI_VERSION = 1

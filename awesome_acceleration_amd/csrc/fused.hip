@@ -1,0 +1,360 @@
+// Fused elementwise kernels around the attention call site (gfx950).
+//
+// The reference runs these as chains of small torch kernels per layer:
+//   RMSNorm                  model/model.py:47-52   (fp32 statistics, result
+//                            cast to the activation dtype, times the weight)
+//   residual add             model/model.py:259, :265 / llm.py:188, :194
+//   q/k RMSNorm + RoPE       model/model.py:225-228 (rotation in the
+//                            activation dtype, model/model.py:86-99)
+//   KV store / append        llm.py:171-174, model/model.py:233-240
+//   SiLU(gate) * up          model/model.py:190
+// Here each chain is one launch.  Every value is rounded to the activation
+// dtype at the same points as the torch expression it replaces, so the fused
+// results equal the unfused ones up to fp32 summation order inside the norm.
+//
+// All three kernels are HBM-bound streaming passes (one read and one write of
+// each tensor).
+
+#include "aac_common.h"
+
+namespace aac {
+
+constexpr int kHeadDimFused = 128;
+
+namespace fz {
+
+template <Dt DT> struct Cvt;
+template <> struct Cvt<Dt::BF16> {
+  __device__ static inline float lo(u32 w) { return bf16lo(w); }
+  __device__ static inline float hi(u32 w) { return bf16hi(w); }
+  __device__ static inline u32 pack(float a, float b) { return pack_bf16x2(a, b); }
+  __device__ static inline float round(float x) { return __uint_as_float(f32_to_bf16_bits(x) << 16); }
+};
+template <> struct Cvt<Dt::FP16> {
+  __device__ static inline float lo(u32 w) { return f16lo(w); }
+  __device__ static inline float hi(u32 w) { return f16hi(w); }
+  __device__ static inline u32 pack(float a, float b) { return pack_f16x2(a, b); }
+  __device__ static inline float round(float x) { return (float)(_Float16)x; }
+};
+
+template <Dt DT>
+__device__ __forceinline__ void unpack8(const u32x4& w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = Cvt<DT>::lo(w[i]);
+    f[2 * i + 1] = Cvt<DT>::hi(w[i]);
+  }
+}
+template <Dt DT>
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = Cvt<DT>::pack(f[2 * i], f[2 * i + 1]);
+  return w;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row16_sum(x);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// One wavefront per row; lane owns 8 consecutive elements per 512-element
+// chunk.  With a residual: h = x + residual (rounded), residual_out = h.
+template <Dt DT, bool RESID, int MAXC>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, int64_t x_stride,
+                                                      const u16* res, u16* res_out,
+                                                      const u16* w, u16* out, int64_t rows,
+                                                      int hidden, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nc = hidden / 512;  // full 512-element chunks
+  float v[MAXC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    if (c < nc) {
+      const int e = c * 512 + lane * 8;
+      unpack8<DT>(*reinterpret_cast<const u32x4*>(x + row * x_stride + e), v[c]);
+      if (RESID) {
+        float r[8];
+        unpack8<DT>(*reinterpret_cast<const u32x4*>(res + row * hidden + e), r);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[c][i] = Cvt<DT>::round(v[c][i] + r[i]);
+        *reinterpret_cast<u32x4*>(res_out + row * hidden + e) = pack8<DT>(v[c]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(v[c][i], v[c][i], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float rs = __frsqrt_rn(ss / (float)hidden + eps);
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    if (c < nc) {
+      const int e = c * 512 + lane * 8;
+      float wf[8], o[8];
+      unpack8<DT>(*reinterpret_cast<const u32x4*>(w + e), wf);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = wf[i] * Cvt<DT>::round(v[c][i] * rs);
+      *reinterpret_cast<u32x4*>(out + row * hidden + e) = pack8<DT>(o);
+    }
+  }
+}
+
+// ------------------------------------------------- q/k RMSNorm + RoPE + store
+struct QkArgs {
+  const u16* qkv;
+  int64_t qkv_stride;  // elements between tokens
+  int64_t n_tokens;
+  int32_t hq, hkv;
+  const u16* qw;  // q_norm weight [128]
+  const u16* kw;  // k_norm weight [128]
+  float eps;
+  const u16* cos;  // [max_pos, 128]
+  const u16* sin;
+  const int32_t* positions;  // [T]
+  int32_t max_pos;
+  u16* q_out;  // [T, hq, 128]
+  u16* k_out;  // [T, hkv, 128] or null
+  u16* k_cache;
+  u16* v_cache;  // rows [*, hkv, 128]; null: no store
+  const int64_t* slot_mapping;  // explicit rows, or null: paged append
+  int64_t num_rows;
+  const int32_t* block_tables;
+  int32_t max_blocks;
+  const int32_t* cache_seqlens;  // append position of token t (= sequence t)
+  int32_t block_size;
+  int64_t num_blocks;
+};
+
+// One 16-lane DPP row per (token, head); lane li owns dims [8li, 8li+8).
+// Rows 0..hq-1 are query heads, hq..hq+hkv-1 key heads, then value heads
+// (value rows are only copied into the cache).
+template <Dt DT>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int heads = a.hq + 2 * a.hkv;
+  const int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // (token, head)
+  const int64_t t = item / heads;
+  const int hh = (int)(item - t * heads);
+  const bool ok = t < a.n_tokens;
+  const int64_t tc = ok ? t : a.n_tokens - 1;  // keep the DPP row fully active
+  const u16* src = a.qkv + tc * a.qkv_stride + (int64_t)hh * kHeadDimFused + li * 8;
+  float x[8];
+  unpack8<DT>(*reinterpret_cast<const u32x4*>(src), x);
+
+  // destination cache row of this token (k/v store)
+  int64_t crow = -1;
+  if (a.v_cache != nullptr && hh >= a.hq) {
+    if (a.slot_mapping != nullptr) {
+      crow = a.slot_mapping[tc];
+      if (crow >= a.num_rows) crow = -1;
+    } else {
+      const int p = a.cache_seqlens[tc];
+      if (p >= 0 && (int64_t)p < (int64_t)a.max_blocks * a.block_size) {
+        const int blk = a.block_tables[tc * a.max_blocks + p / a.block_size];
+        if (blk >= 0 && blk < a.num_blocks) crow = (int64_t)blk * a.block_size + p % a.block_size;
+      }
+    }
+  }
+
+  if (hh >= a.hq + a.hkv) {  // value head: copy to the cache
+    if (ok && crow >= 0)
+      *reinterpret_cast<u32x4*>(a.v_cache + (crow * a.hkv + (hh - a.hq - a.hkv)) * kHeadDimFused +
+                                li * 8) = *reinterpret_cast<const u32x4*>(src);
+    return;
+  }
+  const bool is_q = hh < a.hq;
+  // RMSNorm over the head (model/model.py:47-52)
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+  ss = row16_sum(ss);
+  const float rs = __frsqrt_rn(ss / (float)kHeadDimFused + a.eps);
+  float wf[8];
+  unpack8<DT>(*reinterpret_cast<const u32x4*>((is_q ? a.qw : a.kw) + li * 8), wf);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = Cvt<DT>::round(wf[i] * Cvt<DT>::round(x[i] * rs));
+  // RoPE: out = x*cos + rotate_half(x)*sin, each product and the sum rounded
+  // (model/model.py:90-99); rotate_half pairs dim d with d +- 64, i.e. lane
+  // li with lane li ^ 8 (DPP row_ror:8)
+  int p = a.positions[tc];
+  p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
+  float cf[8], sf[8];
+  unpack8<DT>(*reinterpret_cast<const u32x4*>(a.cos + (int64_t)p * kHeadDimFused + li * 8), cf);
+  unpack8<DT>(*reinterpret_cast<const u32x4*>(a.sin + (int64_t)p * kHeadDimFused + li * 8), sf);
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float partner = __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(x[i]), 0x128, 0xF, 0xF, false));
+    const float rot = li < 8 ? -partner : partner;
+    o[i] = Cvt<DT>::round(Cvt<DT>::round(x[i] * cf[i]) + Cvt<DT>::round(rot * sf[i]));
+  }
+  if (!ok) return;
+  const u32x4 packed = pack8<DT>(o);
+  if (is_q) {
+    *reinterpret_cast<u32x4*>(a.q_out + (t * a.hq + hh) * kHeadDimFused + li * 8) = packed;
+  } else {
+    const int kh = hh - a.hq;
+    if (a.k_out != nullptr)
+      *reinterpret_cast<u32x4*>(a.k_out + (t * a.hkv + kh) * kHeadDimFused + li * 8) = packed;
+    if (crow >= 0)
+      *reinterpret_cast<u32x4*>(a.k_cache + (crow * a.hkv + kh) * kHeadDimFused + li * 8) = packed;
+  }
+}
+
+// ---------------------------------------------------------------- SiLU * up
+template <Dt DT>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const u16* gu, u16* out, int64_t rows,
+                                                       int inter) {
+  const int64_t per_row = inter / 8;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * per_row) return;
+  const int64_t r = i / per_row, c = (i - r * per_row) * 8;
+  float g[8], u[8], o[8];
+  unpack8<DT>(*reinterpret_cast<const u32x4*>(gu + r * 2 * inter + c), g);
+  unpack8<DT>(*reinterpret_cast<const u32x4*>(gu + r * 2 * inter + inter + c), u);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float s = Cvt<DT>::round(g[k] / (1.f + __expf(-g[k])));  // F.silu, rounded
+    o[k] = s * u[k];
+  }
+  *reinterpret_cast<u32x4*>(out + r * inter + c) = pack8<DT>(o);
+}
+
+}  // namespace fz
+}  // namespace aac
+
+using namespace aac;
+
+static bool fz_dtype(int32_t dtype, Dt* dt) {
+  if (dtype == AAC_DTYPE_BF16) { *dt = Dt::BF16; return true; }
+  if (dtype == AAC_DTYPE_FP16) { *dt = Dt::FP16; return true; }
+  return false;
+}
+
+static int fz_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AAC_OK : (int)e;
+}
+
+extern "C" int aac_rmsnorm(const void* x, int64_t x_row_stride, const void* residual,
+                           void* residual_out, const void* weight, void* out, int64_t n_rows,
+                           int32_t hidden, float eps, int32_t dtype, void* stream) {
+  Dt dt;
+  if (!fz_dtype(dtype, &dt)) return AAC_ERR_UNSUPPORTED;
+  if (n_rows < 0 || hidden <= 0 || x_row_stride < hidden) return AAC_ERR_INVALID_ARGUMENT;
+  if (hidden % 512 || hidden > 4096) return AAC_ERR_UNSUPPORTED;
+  if (n_rows == 0) return AAC_OK;
+  if (!x || !weight || !out || ((residual == nullptr) != (residual_out == nullptr)))
+    return AAC_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)residual |
+       (uintptr_t)residual_out) % 16 || x_row_stride % 8)
+    return AAC_ERR_MISALIGNED;
+  const dim3 grid((unsigned)cdiv(n_rows, 4));
+  auto* xs = (const u16*)x;
+  auto* rs = (const u16*)residual;
+  auto* ro = (u16*)residual_out;
+  auto* w = (const u16*)weight;
+  auto* o = (u16*)out;
+  hipStream_t s = (hipStream_t)stream;
+#define AAC_RMS(DTV, R)                                                                         \
+  hipLaunchKernelGGL((fz::rmsnorm_kernel<DTV, R, 8>), grid, dim3(256), 0, s, xs, x_row_stride, rs, \
+                     ro, w, o, n_rows, hidden, eps)
+  if (dt == Dt::BF16) {
+    if (residual) AAC_RMS(Dt::BF16, true); else AAC_RMS(Dt::BF16, false);
+  } else {
+    if (residual) AAC_RMS(Dt::FP16, true); else AAC_RMS(Dt::FP16, false);
+  }
+#undef AAC_RMS
+  return fz_status();
+}
+
+extern "C" int aac_qk_norm_rope_store(
+    const void* qkv, int64_t qkv_tok_stride, int64_t n_tokens, int32_t n_q_heads,
+    int32_t n_kv_heads, int32_t head_dim, const void* q_norm_weight, const void* k_norm_weight,
+    float eps, const void* cos_table, const void* sin_table, int32_t max_position,
+    const int32_t* positions, void* q_out, void* k_out, void* k_cache, void* v_cache,
+    int64_t num_cache_rows, const int64_t* slot_mapping, const int32_t* block_tables,
+    int32_t max_blocks_per_seq, const int32_t* cache_seqlens, int32_t block_size, int32_t dtype,
+    void* stream) {
+  Dt dt;
+  if (!fz_dtype(dtype, &dt)) return AAC_ERR_UNSUPPORTED;
+  if (head_dim != kHeadDimFused) return AAC_ERR_UNSUPPORTED;
+  if (n_tokens < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_position <= 0)
+    return AAC_ERR_INVALID_ARGUMENT;
+  if (qkv_tok_stride < (int64_t)(n_q_heads + 2 * n_kv_heads) * head_dim) return AAC_ERR_SHAPE;
+  if (n_tokens == 0) return AAC_OK;
+  if (!qkv || !q_norm_weight || !k_norm_weight || !cos_table || !sin_table || !positions || !q_out)
+    return AAC_ERR_INVALID_ARGUMENT;
+  const bool store = v_cache != nullptr;
+  if (store) {
+    if (!k_cache) return AAC_ERR_INVALID_ARGUMENT;
+    if (!slot_mapping) {
+      if (!block_tables || !cache_seqlens || block_size <= 0 || max_blocks_per_seq <= 0)
+        return AAC_ERR_INVALID_ARGUMENT;
+    }
+  }
+  if (((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)k_out | (uintptr_t)k_cache |
+       (uintptr_t)v_cache | (uintptr_t)cos_table | (uintptr_t)sin_table) % 16 ||
+      qkv_tok_stride % 8)
+    return AAC_ERR_MISALIGNED;
+  fz::QkArgs a;
+  a.qkv = (const u16*)qkv;
+  a.qkv_stride = qkv_tok_stride;
+  a.n_tokens = n_tokens;
+  a.hq = n_q_heads;
+  a.hkv = n_kv_heads;
+  a.qw = (const u16*)q_norm_weight;
+  a.kw = (const u16*)k_norm_weight;
+  a.eps = eps;
+  a.cos = (const u16*)cos_table;
+  a.sin = (const u16*)sin_table;
+  a.positions = positions;
+  a.max_pos = max_position;
+  a.q_out = (u16*)q_out;
+  a.k_out = (u16*)k_out;
+  a.k_cache = (u16*)k_cache;
+  a.v_cache = (u16*)v_cache;
+  a.slot_mapping = slot_mapping;
+  a.num_rows = num_cache_rows;
+  a.block_tables = block_tables;
+  a.max_blocks = max_blocks_per_seq;
+  a.cache_seqlens = cache_seqlens;
+  a.block_size = block_size;
+  a.num_blocks = block_size > 0 ? num_cache_rows / block_size : 0;
+  const int64_t items = n_tokens * (n_q_heads + 2 * n_kv_heads);
+  const dim3 grid((unsigned)cdiv(items * 16, 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (dt == Dt::BF16)
+    hipLaunchKernelGGL((fz::qk_norm_rope_kernel<Dt::BF16>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((fz::qk_norm_rope_kernel<Dt::FP16>), grid, dim3(256), 0, s, a);
+  return fz_status();
+}
+
+extern "C" int aac_silu_mul(const void* gate_up, void* out, int64_t n_rows, int32_t intermediate,
+                            int32_t dtype, void* stream) {
+  Dt dt;
+  if (!fz_dtype(dtype, &dt)) return AAC_ERR_UNSUPPORTED;
+  if (n_rows < 0 || intermediate <= 0) return AAC_ERR_INVALID_ARGUMENT;
+  if (intermediate % 8) return AAC_ERR_UNSUPPORTED;
+  if (n_rows == 0) return AAC_OK;
+  if (!gate_up || !out) return AAC_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)gate_up | (uintptr_t)out) % 16) return AAC_ERR_MISALIGNED;
+  const dim3 grid((unsigned)cdiv(n_rows * (intermediate / 8), 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (dt == Dt::BF16)
+    hipLaunchKernelGGL((fz::silu_mul_kernel<Dt::BF16>), grid, dim3(256), 0, s,
+                       (const u16*)gate_up, (u16*)out, n_rows, intermediate);
+  else
+    hipLaunchKernelGGL((fz::silu_mul_kernel<Dt::FP16>), grid, dim3(256), 0, s,
+                       (const u16*)gate_up, (u16*)out, n_rows, intermediate);
+  return fz_status();
+}

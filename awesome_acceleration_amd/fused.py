@@ -1,0 +1,109 @@
+"""Python surface of the fused call-site kernels (RMSNorm + residual, q/k
+RMSNorm + RoPE + KV store, SiLU * up).  Device tensors only; every op runs on
+the current stream and fails loudly without the HIP library."""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+__all__ = ["rmsnorm", "qk_norm_rope_store", "silu_mul"]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _req(cond: bool, msg: str):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _code(t: torch.Tensor) -> int:
+    _req(t.dtype in (torch.bfloat16, torch.float16), f"unsupported dtype {t.dtype}")
+    return _lib.AAC_DTYPE[t.dtype]
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: Optional[torch.Tensor] = None):
+    """RMSNorm of ``x`` [rows, hidden] (model/model.py:47-52).  With
+    ``residual``: returns ``(norm(x + residual), x + residual)``."""
+    _req(x.is_cuda and x.dim() == 2 and x.stride(1) == 1, "x must be a [rows, hidden] GPU tensor")
+    rows, hidden = x.shape
+    out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
+    res_out = None
+    if residual is not None:
+        _req(residual.shape == x.shape and residual.is_contiguous(), "residual shape")
+        res_out = torch.empty_like(residual)
+    rc = _lib.lib().aac_rmsnorm(
+        x.data_ptr(), x.stride(0), residual.data_ptr() if residual is not None else None,
+        res_out.data_ptr() if res_out is not None else None, weight.data_ptr(), out.data_ptr(),
+        rows, hidden, float(eps), _code(x), _stream(x))
+    _lib.check(rc, "aac_rmsnorm")
+    return out if residual is None else (out, res_out)
+
+
+def qk_norm_rope_store(qkv: torch.Tensor, n_q_heads: int, n_kv_heads: int,
+                       q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
+                       cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                       k_cache: Optional[torch.Tensor] = None,
+                       v_cache: Optional[torch.Tensor] = None,
+                       slot_mapping: Optional[torch.Tensor] = None,
+                       block_tables: Optional[torch.Tensor] = None,
+                       cache_seqlens: Optional[torch.Tensor] = None, want_k: bool = True):
+    """q/k RMSNorm + RoPE of the fused projection ``qkv`` [T, (Hq+2Hkv)*128]
+    (model/model.py:219-228) and, with caches, the K/V store through
+    ``slot_mapping`` (llm.py:171-174) or the decode append at
+    ``cache_seqlens`` of ``block_tables`` (model/model.py:233-240).
+    Returns ``(q [T,Hq,128], k [T,Hkv,128] or None)``."""
+    _req(qkv.is_cuda and qkv.dim() == 2 and qkv.stride(1) == 1, "qkv must be [T, width]")
+    T = qkv.shape[0]
+    D = 128
+    _req(qkv.shape[1] == (n_q_heads + 2 * n_kv_heads) * D, "qkv width")
+    _req(positions.dtype == torch.int32 and positions.shape == (T,), "positions must be int32 [T]")
+    q = torch.empty((T, n_q_heads, D), dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty((T, n_kv_heads, D), dtype=qkv.dtype, device=qkv.device) if want_k else None
+    rows = 0
+    bs = 0
+    mb = 0
+    if v_cache is not None:
+        _req(k_cache is not None and k_cache.shape == v_cache.shape and k_cache.is_contiguous()
+             and v_cache.is_contiguous(), "caches must be contiguous and alike")
+        rows = k_cache.numel() // (n_kv_heads * D)
+        if slot_mapping is None:
+            _req(block_tables is not None and cache_seqlens is not None,
+                 "append needs block_tables and cache_seqlens")
+            _req(block_tables.dtype == torch.int32 and block_tables.is_contiguous()
+                 and block_tables.shape[0] == T, "block_tables must be int32 [T, W]")
+            _req(cache_seqlens.dtype == torch.int32 and cache_seqlens.shape == (T,),
+                 "cache_seqlens must be int32 [T]")
+            bs = k_cache.shape[1]
+            mb = block_tables.shape[1]
+        else:
+            _req(slot_mapping.dtype == torch.int64 and slot_mapping.shape == (T,),
+                 "slot_mapping must be int64 [T]")
+    rc = _lib.lib().aac_qk_norm_rope_store(
+        qkv.data_ptr(), qkv.stride(0), T, n_q_heads, n_kv_heads, D, q_norm_weight.data_ptr(),
+        k_norm_weight.data_ptr(), float(eps), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+        positions.data_ptr(), q.data_ptr(), k.data_ptr() if k is not None else None,
+        k_cache.data_ptr() if v_cache is not None else None,
+        v_cache.data_ptr() if v_cache is not None else None, rows,
+        slot_mapping.data_ptr() if slot_mapping is not None else None,
+        block_tables.data_ptr() if (v_cache is not None and slot_mapping is None) else None, mb,
+        cache_seqlens.data_ptr() if (v_cache is not None and slot_mapping is None) else None, bs,
+        _code(qkv), _stream(qkv))
+    _lib.check(rc, "aac_qk_norm_rope_store")
+    return q, k
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """``silu(gate) * up`` of the fused [gate | up] projection (model/model.py:190)."""
+    _req(gate_up.is_cuda and gate_up.dim() == 2 and gate_up.is_contiguous(), "gate_up [rows, 2I]")
+    rows, two_i = gate_up.shape
+    out = torch.empty((rows, two_i // 2), dtype=gate_up.dtype, device=gate_up.device)
+    rc = _lib.lib().aac_silu_mul(gate_up.data_ptr(), out.data_ptr(), rows, two_i // 2,
+                                 _code(gate_up), _stream(gate_up))
+    _lib.check(rc, "aac_silu_mul")
+    return out

@@ -85,7 +85,8 @@ class LLM:
     def __init__(self, config: Optional[Qwen3Config] = None, max_num_seqs: int = 32,
                  max_seq_len: int = 4096, dtype=torch.bfloat16, block_size: int = 256,
                  num_blocks: Optional[int] = None, seed: int = 0, device="cuda",
-                 decode_fn: Optional[Callable[[list[int]], str]] = None, use_graphs: bool = True):
+                 decode_fn: Optional[Callable[[list[int]], str]] = None, use_graphs: bool = True,
+                 fused: bool = True):
         self.device = torch.device(device)
         self.dtype = dtype
         self.config = config or Qwen3Config()
@@ -96,7 +97,7 @@ class LLM:
         if num_blocks is None:
             num_blocks = max_num_seqs * self.blocks_per_seq
         self.decode_fn = decode_fn
-        self.model = Qwen3ForCausalLM(self.config, self.device, dtype, seed)
+        self.model = Qwen3ForCausalLM(self.config, self.device, dtype, seed, fused=fused)
         # block 0 is a scratch block: padding rows of a graph-captured decode
         # step append into it, so they never touch a live sequence's cache
         self.cache = PagedKVCache(self.config, num_blocks + 1, block_size, self.device, dtype)
@@ -104,10 +105,10 @@ class LLM:
         self.allocator.allocate(1)
         self.use_graphs = use_graphs
         self._graphs: dict[int, tuple] = {}
-        # packed per-step host metadata: ids | positions | seqlens | tables
+        # packed per-step host metadata: ids | positions | seqlens | ctx | tables
         W = self.blocks_per_seq
-        self._host = torch.zeros(max_num_seqs * (3 + W), dtype=torch.int32, pin_memory=True)
-        self._dev = torch.zeros(max_num_seqs * (3 + W), dtype=torch.int32, device=self.device)
+        self._host = torch.zeros(max_num_seqs * (4 + W), dtype=torch.int32, pin_memory=True)
+        self._dev = torch.zeros(max_num_seqs * (4 + W), dtype=torch.int32, device=self.device)
         self._request_queue: queue.Queue[_Request] = queue.Queue()
         self._loop_running = False
         self._loop_thread: Optional[threading.Thread] = None
@@ -174,7 +175,8 @@ class LLM:
     def _decode_meta(self, B: int, max_context_len: int) -> StepMeta:
         d, W = self._dev, self.blocks_per_seq
         return StepMeta(positions=d[B:2 * B], cache_seqlens=d[2 * B:3 * B],
-                        block_tables=d[3 * B:3 * B + B * W].view(B, W),
+                        context_lens=d[3 * B:4 * B],
+                        block_tables=d[4 * B:4 * B + B * W].view(B, W),
                         max_context_len=max_context_len)
 
     def _decode_step(self, seqs: list[_Seq]) -> torch.Tensor:
@@ -187,14 +189,15 @@ class LLM:
         n, W = len(seqs), self.blocks_per_seq
         B = min(1 << (n - 1).bit_length(), self.max_num_seqs) if self.use_graphs else n
         h = self._host.numpy()
-        h[:3 * B + B * W] = 0
+        h[:4 * B + B * W] = 0
         h[:n] = [s.tokens[-1] for s in seqs]
         h[B:B + n] = [s.pos for s in seqs]
         h[2 * B:2 * B + n] = [s.pos for s in seqs]  # tokens already in the cache
-        tab = h[3 * B:3 * B + B * W].reshape(B, W)
+        h[3 * B:4 * B] = h[2 * B:3 * B] + 1           # context after the append
+        tab = h[4 * B:4 * B + B * W].reshape(B, W)
         for i, s in enumerate(seqs):
             tab[i, :len(s.blocks)] = s.blocks
-        m = B * (3 + W)
+        m = B * (4 + W)
         self._dev[:m].copy_(self._host[:m], non_blocking=True)
         self.stats["decode_steps"] += 1
         self.stats["decode_tokens"] += n

@@ -32,6 +32,7 @@ import torch
 import torch.nn.functional as F
 
 from . import flash_attn_interface as fai
+from . import fused as fz
 
 __all__ = ["Qwen3Config", "Qwen3ForCausalLM", "PagedKVCache", "StepMeta"]
 
@@ -120,8 +121,9 @@ class StepMeta:
 
     prefill: ``cu_seqlens`` int32 [n+1], ``positions`` int64 [N],
              ``slot_mapping`` int64 [N], ``max_seqlen``, ``last_idx`` int64 [n]
-    decode:  ``positions`` int64 [B], ``block_tables`` int32 [B, W],
+    decode:  ``positions`` int32 [B], ``block_tables`` int32 [B, W],
              ``cache_seqlens`` int32 [B] (length before this step's append),
+             ``context_lens`` int32 [B] (= cache_seqlens + 1),
              ``max_context_len`` (upper bound on cache_seqlens + 1)
     """
     positions: torch.Tensor
@@ -131,14 +133,17 @@ class StepMeta:
     last_idx: torch.Tensor | None = None
     block_tables: torch.Tensor | None = None
     cache_seqlens: torch.Tensor | None = None
+    context_lens: torch.Tensor | None = None
     max_context_len: int = 0
 
 
 class Qwen3ForCausalLM:
     """Random-initialised Qwen3 with tied embeddings (model/model.py:289-322)."""
 
-    def __init__(self, cfg: Qwen3Config, device, dtype=torch.bfloat16, seed: int = 0):
+    def __init__(self, cfg: Qwen3Config, device, dtype=torch.bfloat16, seed: int = 0,
+                 fused: bool = True):
         self.cfg = cfg
+        self.fused = fused
         self.device = torch.device(device)
         self.dtype = dtype
         self.hq, self.hkv, self.d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -218,12 +223,54 @@ class Qwen3ForCausalLM:
         h = res + self._mlp(L, rms_norm(h, L["ln2"], eps))
         return h
 
+    def _forward_fused(self, input_ids, meta: StepMeta, cache: PagedKVCache, prefill: bool):
+        """The same layer with the fused call-site kernels: residual add +
+        RMSNorm, q/k RMSNorm + RoPE + KV store/append, SiLU * up are one launch
+        each, and the residual add of each block is folded into the next norm."""
+        eps = self.cfg.rms_norm_eps
+        I = self.cfg.intermediate_size
+        h = F.embedding(input_ids, self.embed)
+        res, delta = h, None
+        T = h.shape[0]
+        pos = meta.positions if meta.positions.dtype == torch.int32 else meta.positions.int()
+        for li, L in enumerate(self.layers):
+            if delta is None:
+                x = fz.rmsnorm(res, L["ln1"], eps)
+            else:
+                x, res = fz.rmsnorm(delta, L["ln1"], eps, residual=res)
+            qkv = F.linear(x, L["qkv"])
+            if prefill:
+                q, k = fz.qk_norm_rope_store(
+                    qkv, self.hq, self.hkv, L["q_norm"], L["k_norm"], eps, self.rope.cos,
+                    self.rope.sin, pos, cache.k(li), cache.v(li), slot_mapping=meta.slot_mapping)
+                v = qkv[:, self.q_size + self.kv_size:].view(T, self.hkv, self.d)
+                attn = fai.flash_attn_varlen_func(q, k, v, meta.cu_seqlens, meta.cu_seqlens,
+                                                  meta.max_seqlen, meta.max_seqlen,
+                                                  softmax_scale=self.scale, causal=True)
+            else:
+                q, _ = fz.qk_norm_rope_store(
+                    qkv, self.hq, self.hkv, L["q_norm"], L["k_norm"], eps, self.rope.cos,
+                    self.rope.sin, pos, cache.k(li), cache.v(li), block_tables=meta.block_tables,
+                    cache_seqlens=meta.cache_seqlens, want_k=False)
+                attn = fai.decode_paged(q, cache.k(li), cache.v(li), meta.block_tables,
+                                        meta.context_lens, softmax_scale=self.scale,
+                                        max_context_len=meta.max_context_len)
+            o = F.linear(attn.reshape(T, -1), L["o"])
+            x, res = fz.rmsnorm(o, L["ln2"], eps, residual=res)
+            delta = F.linear(fz.silu_mul(F.linear(x, L["gate_up"])), L["down"])
+        if prefill:
+            delta, res = delta[meta.last_idx], res[meta.last_idx]
+        h, _ = fz.rmsnorm(delta, self.norm, eps, residual=res)
+        return F.linear(h, self.embed)  # tied embeddings
+
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor, meta: StepMeta, cache: PagedKVCache,
                 prefill: bool) -> torch.Tensor:
         """Logits for the last token of every sequence: prefill takes packed
         tokens (llm.py:116-208), decode one token per sequence
         (model/model.py:302-322)."""
+        if self.fused:
+            return self._forward_fused(input_ids, meta, cache, prefill)
         h = F.embedding(input_ids, self.embed)
         for li in range(self.cfg.num_hidden_layers):
             h = self._layer(li, h, meta, cache, prefill)

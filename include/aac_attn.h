@@ -192,6 +192,57 @@ int aac_decode_append_paged(const void* q, int64_t q_seq_stride, const void* k, 
                             size_t workspace_bytes, int32_t partition_tokens, int32_t dtype,
                             void* stream);
 
+/* ------------------------------------------------------------------------
+ * Fused kernels of the attention call site.  Each replaces a chain of small
+ * torch kernels of the reference layer with one launch and rounds to the
+ * activation dtype at the same points.  dtype: BF16 or FP16.
+ * ---------------------------------------------------------------------- */
+
+/*
+ * out = weight * dtype(h * rsqrt(mean(h^2) + eps)), statistics in fp32, where
+ * h = x, or h = dtype(x + residual) with residual_out = h when residual is
+ * given (residual and residual_out together or neither).  x rows have stride
+ * x_row_stride; residual, residual_out and out are contiguous [n_rows, hidden].
+ * hidden must be a multiple of 512, at most 4096.
+ * Replaces RMSNorm (model/model.py:47-52) and the residual add before it
+ * (model/model.py:259, :265; llm.py:188, :194).
+ */
+int aac_rmsnorm(const void* x, int64_t x_row_stride, const void* residual, void* residual_out,
+                const void* weight, void* out, int64_t n_rows, int32_t hidden, float eps,
+                int32_t dtype, void* stream);
+
+/*
+ * Per token of the fused QKV projection qkv [n_tokens, (Hq + 2*Hkv) * 128]
+ * (row stride qkv_tok_stride): RMSNorm of every q and k head with
+ * q_norm_weight / k_norm_weight, then RoPE with the cos/sin tables
+ * [max_position, 128] at positions[t] (x*cos + rotate_half(x)*sin, each term
+ * rounded), writing q_out [n_tokens, Hq, 128] and, if k_out is given,
+ * k_out [n_tokens, Hkv, 128].  If v_cache is given the rotated k and the raw v
+ * of token t are stored in the caches (rows [*, Hkv, 128]): at row
+ * slot_mapping[t] (negative or >= num_cache_rows: skipped), or, when
+ * slot_mapping is NULL, appended at position cache_seqlens[t] of block table
+ * row t (decode: token t is sequence t).
+ * Replaces model/model.py:219-228 plus the KV store llm.py:171-174 /
+ * the k=/v= append of flash_attn_with_kvcache (model/model.py:233-240).
+ */
+int aac_qk_norm_rope_store(const void* qkv, int64_t qkv_tok_stride, int64_t n_tokens,
+                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           const void* q_norm_weight, const void* k_norm_weight, float eps,
+                           const void* cos_table, const void* sin_table, int32_t max_position,
+                           const int32_t* positions, void* q_out, void* k_out, void* k_cache,
+                           void* v_cache, int64_t num_cache_rows, const int64_t* slot_mapping,
+                           const int32_t* block_tables, int32_t max_blocks_per_seq,
+                           const int32_t* cache_seqlens, int32_t block_size, int32_t dtype,
+                           void* stream);
+
+/*
+ * out[r, i] = dtype(silu(gate_up[r, i])) * gate_up[r, intermediate + i] for the
+ * fused [gate | up] projection gate_up [n_rows, 2*intermediate].
+ * Replaces act_fn(gate_proj(x)) * up_proj(x) (model/model.py:190).
+ */
+int aac_silu_mul(const void* gate_up, void* out, int64_t n_rows, int32_t intermediate,
+                 int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

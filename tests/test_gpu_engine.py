@@ -66,20 +66,21 @@ def _prompts(n, seed):
     return [rs.randint(0, CFG.vocab_size, rs.randint(1, 300)).tolist() for _ in range(n)]
 
 
-def _run(use_graphs, prompts, max_tokens, max_num_seqs=4):
+def _run(use_graphs, prompts, max_tokens, max_num_seqs=4, fused=True):
     llm = LLM(CFG, max_num_seqs=max_num_seqs, max_seq_len=512, block_size=64, seed=0,
-              use_graphs=use_graphs)
+              use_graphs=use_graphs, fused=fused)
     futs = [llm.generate([p], max_tokens=mt, ignore_eos=True) for p, mt in zip(prompts, max_tokens)]
     outs = [f.result(timeout=120)[0] for f in futs]
     llm.stop()
     return llm, outs
 
 
-def test_engine_tokens_match_reference_and_graphs_match_eager(gpu):
-    print("case: engine continuous batching vs fp32 reference", flush=True)
+@pytest.mark.parametrize("fused", [True, False])
+def test_engine_tokens_match_reference_and_graphs_match_eager(gpu, fused):
+    print(f"case: engine continuous batching vs fp32 reference (fused={fused})", flush=True)
     prompts = _prompts(9, 0)
     max_tokens = [1, 5, 12, 3, 20, 8, 2, 15, 6]
-    llm, eager = _run(False, prompts, max_tokens)
+    llm, eager = _run(False, prompts, max_tokens, fused=fused)
     assert [o.generated_tokens for o in eager] == max_tokens
     assert all(o.prompt_tokens == len(p) for o, p in zip(eager, prompts))
     checked = 0
@@ -95,7 +96,7 @@ def test_engine_tokens_match_reference_and_graphs_match_eager(gpu):
     assert checked >= 0.5 * sum(max_tokens), checked
     print(f"checked {checked} tokens against the reference", flush=True)
     # graph-captured decode (power-of-two buckets, padding rows) == eager
-    _, graphed = _run(True, prompts, max_tokens)
+    _, graphed = _run(True, prompts, max_tokens, fused=fused)
     assert [o.token_ids for o in graphed] == [o.token_ids for o in eager]
 
 

@@ -1,0 +1,117 @@
+"""Fused call-site kernels against the reference's own torch expressions:
+RMSNorm (model/model.py:47-52) with the residual add before it, q/k RMSNorm +
+RoPE (model/model.py:86-99, :225-228) with the KV store (llm.py:171-174) or
+decode append, and SiLU * up (model/model.py:190).  The fused kernels round at
+the same points, so results match to one unit in the last place where fp32
+summation order differs, and the cache stores are bit-exact."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from awesome_acceleration_amd import fused as fz
+from awesome_acceleration_amd.qwen3 import Rope, rms_norm
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp_close(a: torch.Tensor, b: torch.Tensor, what: str, max_frac: float = 2e-2):
+    """Equal except for at most ``max_frac`` of the elements, each within a
+    few units in the last place.  A one-ulp difference in the normalised value
+    (fp32 summation order, correctly rounded vs. library rsqrt) can move a
+    later rounded product or sum (x weight, x cos, + rotated term) by up to
+    two ulps of the result; the bound allows four, relative to the larger
+    magnitude, plus the subnormal spacing."""
+    mant = 8 if a.dtype == torch.bfloat16 else 11  # significand bits
+    tiny = 2.0 ** -133 if a.dtype == torch.bfloat16 else 2.0 ** -24
+    a, b = a.float(), b.float()
+    assert torch.isfinite(a).all(), what
+    tol = torch.maximum(a.abs(), b.abs()) * 2.0 ** -(mant - 3) + 4 * tiny
+    diff = (a - b).abs()
+    assert (diff <= tol).all(), f"{what}: max diff {float(diff.max()):.3e}"
+    frac = float((diff > 0).float().mean())
+    assert frac <= max_frac, f"{what}: {frac:.4%} elements differ"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hidden", [1024, 4096])
+def test_rmsnorm_with_and_without_residual(gpu, dtype, hidden):
+    print(f"case: rmsnorm {dtype} {hidden}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(0)
+    rows = 300
+    x = torch.randn((rows, hidden), generator=g, device=gpu).to(dtype)
+    r = torch.randn((rows, hidden), generator=g, device=gpu).to(dtype)
+    w = (1 + 0.3 * torch.randn(hidden, generator=g, device=gpu)).to(dtype)
+    out = fz.rmsnorm(x, w, 1e-6)
+    ulp_close(out, rms_norm(x, w, 1e-6), "rmsnorm")
+    out2, h = fz.rmsnorm(x, w, 1e-6, residual=r)
+    assert torch.equal(h, r + x)  # the residual add, rounded like torch
+    ulp_close(out2, rms_norm(r + x, w, 1e-6), "add+rmsnorm")
+    # strided rows (a view into a wider buffer)
+    wide = torch.randn((rows, hidden + 64), generator=g, device=gpu).to(dtype)
+    ulp_close(fz.rmsnorm(wide[:, :hidden], w, 1e-6), rms_norm(wide[:, :hidden], w, 1e-6), "strided")
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8)])
+def test_qk_norm_rope_prefill_store(gpu, hq, hkv):
+    print(f"case: qk norm rope store {hq}/{hkv}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(1)
+    T, D, bs, pool = 777, 128, 64, 20
+    qkv = torch.randn((T, (hq + 2 * hkv) * D), generator=g, device=gpu).to(torch.bfloat16)
+    qw = (1 + 0.3 * torch.randn(D, generator=g, device=gpu)).to(torch.bfloat16)
+    kw = (1 + 0.3 * torch.randn(D, generator=g, device=gpu)).to(torch.bfloat16)
+    rope = Rope(D, 4096, 1e6, gpu, torch.bfloat16)
+    pos = torch.randint(0, 4096, (T,), generator=g, device=gpu, dtype=torch.int32)
+    kc = torch.randn((pool, bs, hkv, D), generator=g, device=gpu).to(torch.bfloat16)
+    vc = torch.randn((pool, bs, hkv, D), generator=g, device=gpu).to(torch.bfloat16)
+    kc0, vc0 = kc.clone(), vc.clone()
+    slots = torch.randperm(pool * bs, generator=g, device=gpu)[:T].to(torch.int64)
+    slots[5] = -1  # padding token: not stored
+    q, k = fz.qk_norm_rope_store(qkv, hq, hkv, qw, kw, 1e-6, rope.cos, rope.sin, pos, kc, vc,
+                                 slot_mapping=slots)
+    torch.cuda.synchronize()
+    qr = rope.apply(rms_norm(qkv[:, :hq * D].view(T, hq, D), qw, 1e-6), pos)
+    kr = rope.apply(rms_norm(qkv[:, hq * D:(hq + hkv) * D].view(T, hkv, D), kw, 1e-6), pos)
+    ulp_close(q, qr, "q")
+    ulp_close(k, kr, "k")
+    v = qkv[:, (hq + hkv) * D:].view(T, hkv, D)
+    keep = slots >= 0
+    ek, ev = kc0.view(-1, hkv, D).clone(), vc0.view(-1, hkv, D).clone()
+    ek[slots[keep]] = k[keep]
+    ev[slots[keep]] = v[keep]
+    assert torch.equal(kc.view(-1, hkv, D), ek)  # stored bits are the returned k, untouched rows kept
+    assert torch.equal(vc.view(-1, hkv, D), ev)
+
+
+def test_qk_norm_rope_decode_append(gpu):
+    print("case: qk norm rope append", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(2)
+    B, hq, hkv, D, bs, W = 9, 16, 8, 128, 16, 4
+    qkv = torch.randn((B, (hq + 2 * hkv) * D), generator=g, device=gpu).to(torch.bfloat16)
+    w1 = torch.ones(D, device=gpu, dtype=torch.bfloat16)
+    rope = Rope(D, 1024, 1e6, gpu, torch.bfloat16)
+    pool = B * W
+    bt = torch.randperm(pool, generator=g, device=gpu).view(B, W).to(torch.int32)
+    seqlens = torch.randint(0, W * bs, (B,), generator=g, device=gpu, dtype=torch.int32)
+    kc = torch.zeros((pool, bs, hkv, D), device=gpu, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    q, none = fz.qk_norm_rope_store(qkv, hq, hkv, w1, w1, 1e-6, rope.cos, rope.sin, seqlens, kc,
+                                    vc, block_tables=bt, cache_seqlens=seqlens, want_k=False)
+    torch.cuda.synchronize()
+    assert none is None
+    kr = rope.apply(rms_norm(qkv[:, hq * D:(hq + hkv) * D].view(B, hkv, D), w1, 1e-6), seqlens)
+    v = qkv[:, (hq + hkv) * D:].view(B, hkv, D)
+    btn, sl = bt.cpu().numpy(), seqlens.cpu().numpy()
+    rows = torch.tensor([int(btn[b, sl[b] // bs]) * bs + int(sl[b]) % bs for b in range(B)],
+                        device=gpu)
+    ulp_close(kc.view(-1, hkv, D)[rows], kr, "appended k")
+    assert torch.equal(vc.view(-1, hkv, D)[rows], v)
+    assert int((kc.view(-1, hkv, D).abs().sum((1, 2)) > 0).sum()) == B  # nothing else written
+
+
+def test_silu_mul(gpu):
+    print("case: silu mul", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(3)
+    gu = torch.randn((513, 2 * 3072), generator=g, device=gpu).to(torch.bfloat16)
+    ref = F.silu(gu[:, :3072]) * gu[:, 3072:]
+    ulp_close(fz.silu_mul(gu), ref, "silu*up")
