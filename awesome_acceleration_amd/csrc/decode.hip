@@ -329,11 +329,11 @@ static DecodePlan plan_decode(int32_t n_seqs, int32_t hq, int32_t hkv, int32_t b
   int64_t part = part_tokens;
   if (part <= 0) {
     // Measured on MI355X (bf16, block 256): with >= 1024 (sequence, KV head)
-    // items and contexts up to 2048 tokens one workgroup per item streams at
+    // items and contexts up to 4096 tokens one workgroup per item streams at
     // the HBM ceiling and needs no reduction; otherwise 1024-token partitions,
     // shrunk (down to 256) until there are >= 2048 workgroups for 256 CUs.
     const int64_t items = (int64_t)n_seqs * hkv;
-    if (items >= 1024 && cap <= 2048) {
+    if (items >= 1024 && cap <= 4096) {
       part = cap;
     } else {
       part = 1024;
