@@ -112,6 +112,12 @@ __device__ __forceinline__ float row16_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// IEEE 754-2019 maximum (NaN-propagating).  Unlike fmaxf it needs no
+// canonicalisation of its inputs, and chains of two fold into one
+// v_maximum3_f32 on gfx950.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float vmax3(float a, float b, float c) { return vmax(vmax(a, b), c); }
+
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace aac

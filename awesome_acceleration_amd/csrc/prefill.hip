@@ -26,13 +26,16 @@
 //   * Causal masking is bottom-right aligned (query i sees keys
 //     j <= i + Lk - Lq); key tiles beyond a wave's last visible key are
 //     skipped, and only tiles that cross the diagonal evaluate the mask.
-//   * Grid = (kv head, segment, q-block rank) with the last (heaviest) causal
-//     q-blocks dispatched first.
+//   * Persistent grid, one workgroup per CU: the work items (KV head,
+//     segment, q-block) are taken heaviest causal q-blocks first in a zigzag
+//     that pairs heavy with light items, and each workgroup issues the next
+//     item's Q and first K/V tile before the current item's epilogue.
 //
 // FLOPs per launch (the MFMA roofline): 4 * Hq * D * sum over segments of the
 // visible (query, key) pairs, i.e. 4*Hq*D*L(L+1)/2 per causal segment.
 
 #include <algorithm>
+#include <atomic>
 
 #include "aac_common.h"
 
@@ -43,6 +46,7 @@ namespace pf {
 constexpr int D = 128;
 constexpr int BKV = 64;        // keys per LDS tile (two 32-key sub-tiles)
 constexpr int KPITCH = D + 8;  // K tile row pitch (elements): 8 consecutive rows hit 8 disjoint bank quads
+constexpr int OPITCH = D + 8;  // output staging row pitch (elements)
 constexpr int STAGES = 3;      // LDS ring: one barrier per tile (see the hazard note in the kernel)
 constexpr float kRescale = 8.f;  // lazy-rescale threshold (log2 units): p <= 256
 constexpr int kWaves = 8;        // wavefronts per workgroup (2 per SIMD)
@@ -59,6 +63,7 @@ struct Args {
   int32_t hq, hkv;
   float scale_log2;
   u16* out;
+  int32_t n_qblocks;  // q-blocks of the longest segment
 };
 
 template <bool F16> struct Mfma;
@@ -123,64 +128,29 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   static_assert(WH * WQ == kWaves, "eight waves per workgroup");
   typedef Mfma<F16> M;
 
-  __shared__ __attribute__((aligned(16))) u16 Ks[STAGES][BKV * KPITCH];
-  __shared__ __attribute__((aligned(16))) u16 Vt[STAGES][D * BKV];
+  // LDS: the K / V^T ring, reused after each item to stage the output tile
+  constexpr int kRingElems = STAGES * (BKV * KPITCH + D * BKV);
+  static_assert(kWaves * 32 * OPITCH <= kRingElems, "output staging fits in the ring");
+  __shared__ __attribute__((aligned(16))) u16 lds[kRingElems];
+  auto Ks = [&](int st) { return lds + st * (BKV * KPITCH); };
+  auto Vt = [&](int st) { return lds + STAGES * BKV * KPITCH + st * (D * BKV); };
 
-  const int h = blockIdx.x;
-  const int s = blockIdx.y;
-  const int q_beg = a.cu_q[s], Lq = a.cu_q[s + 1] - q_beg;
-  const int k_beg = a.cu_k[s], Lk = a.cu_k[s + 1] - k_beg;
-  const int nqb = (Lq + BQ - 1) / BQ;
-  const int rank = blockIdx.z;
-  if (rank >= nqb) return;
-  const int qb = CAUSAL ? nqb - 1 - rank : rank;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // The wave index made explicitly wave-uniform: the staging role, buffer
+  // resource, row stride and scalar offsets then live in SGPRs (a per-lane
+  // resource would turn every buffer load into a readfirstlane loop).
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wq = wave % WQ, wh = wave / WQ;
   const int hl = lane >> 5;  // lane half
   const int col = lane & 31;
-  const int qi = qb * BQ + wq * 32 + col;  // query index in the segment
-  const bool q_ok = qi < Lq;
-  const int shift = Lk - Lq;  // bottom-right causal alignment
-
-  // keys visible to the whole workgroup / this wave / this lane
-  const int wg_qmax = min(qb * BQ + BQ, Lq) - 1;
-  const int kv_end = CAUSAL ? max(0, min(Lk, wg_qmax + 1 + shift)) : Lk;
-  const int w_qmin = qb * BQ + wq * 32;
-  const int w_qmax = min(w_qmin + 31, Lq - 1);
-  const int w_end = w_qmin >= Lq ? 0 : (CAUSAL ? max(0, min(Lk, w_qmax + 1 + shift)) : Lk);
-  const int w_full = CAUSAL ? min(Lk, w_qmin + 1 + shift) : Lk;  // keys < w_full need no mask
-  const int my_lim = CAUSAL ? min(Lk, qi + 1 + shift) : Lk;
-  const int nt = (kv_end + BKV - 1) / BKV;  // LDS tiles (workgroup-uniform)
-  const int nsub = (w_end + 31) / 32;       // 32-key sub-tiles this wave computes
-
-  // Q fragments: B operand of S^T = K Q^T, lane = query column, 8 dims.
-  u32x4 qf[8];
-  {
-    const int qrow = q_beg + min(qi, max(Lq - 1, 0));  // clamped: rows >= Lq are never stored
-    const u16* qp = a.q + (int64_t)qrow * a.q_stride + (h * G + wh) * D + hl * 8;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) qf[t] = *reinterpret_cast<const u32x4*>(qp + 16 * t);
-  }
-
-  f32x16 o[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[c][i] = 0.f;
-  float m = -1e30f, l = 0.f;  // m: reference max of the raw scores (scale applied in exp2)
 
   // ---- staging.  Waves 0-3 stage K (thread: rows (tid>>4) + 16*i), waves
   // 4-7 stage V (thread: rows 4*(tid>>4) + i, transposed into V^T), 16 B at
   // dim (tid&15)*8.  Buffer loads return zeros for rows >= kv_end (the
   // resource covers exactly the visible rows), so tails need no clamping.
-  const bool k_role = tid < 256;
+  const bool k_role = wave < 4;
   const int st_r = (tid & 255) >> 4, st_c = (tid & 15) * 8;
-  const int64_t sg_stride = k_role ? a.k_stride : a.v_stride;  // elements
-  const u16* sg_base = (k_role ? a.k + (int64_t)k_beg * a.k_stride : a.v + (int64_t)k_beg * a.v_stride) + h * D;
-  const int row_bytes = (int)(sg_stride * 2);
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<u16*>(sg_base), 0, kv_end > 0 ? (kv_end - 1) * row_bytes + D * 2 : 0, 0x00020000);
+  const int row_bytes = (int)((k_role ? a.k_stride : a.v_stride) * 2);
   // per-thread staging offsets: global (bytes, one VGPR; the row step goes
   // into the scalar offset) and LDS (elements)
   const int st_voff = (k_role ? st_r : st_r * 4) * row_bytes + st_c * 2;
@@ -200,6 +170,72 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     for (int k = 0; k < 4; ++k) v_oct[k] = (x0 ^ (2 * k)) << 3;
   }
 
+  // ---- work items (q-block rank z, segment s, KV head h), numbered
+  // rank-major so that the heaviest causal q-blocks come first.  The grid is
+  // persistent (one workgroup per CU): workgroup w of P takes item k*P + w in
+  // even rounds k and (k+1)*P - 1 - w in odd rounds, a zigzag that pairs
+  // heavy with light items, and skips the ranks a short segment lacks.
+  struct Item {
+    int h, s, qb, q_beg, Lq, k_beg, Lk;
+  };
+  const int n_hs = a.hkv * a.n_seqs;
+  const int n_items = n_hs * a.n_qblocks;
+  const int P = gridDim.x, w = blockIdx.x;
+  auto item_index = [&](int k) { return (k & 1) ? (k + 1) * P - 1 - w : k * P + w; };
+  auto seg_of = [&](int i) { return (i % n_hs) / a.hkv; };
+  // item i from its segment's bounds; false for a rank the segment lacks
+  auto decode = [&](int i, int q0, int q1, int k0, int k1, Item& it) -> bool {
+    const int z = i / n_hs;
+    it.s = (i - z * n_hs) / a.hkv;
+    it.h = i - z * n_hs - it.s * a.hkv;
+    it.q_beg = q0;
+    it.Lq = q1 - q0;
+    it.k_beg = k0;
+    it.Lk = k1 - k0;
+    const int nqb = (it.Lq + BQ - 1) / BQ;
+    it.qb = CAUSAL ? nqb - 1 - z : z;
+    return z < nqb;
+  };
+  // first valid item of round k or later (k is left at its round)
+  auto next_item = [&](int& k, Item& it) -> bool {
+    for (; k * P < n_items; ++k) {
+      const int i = item_index(k);
+      if (i >= n_items) continue;
+      const int sg = seg_of(i);
+      if (decode(i, a.cu_q[sg], a.cu_q[sg + 1], a.cu_k[sg], a.cu_k[sg + 1], it)) return true;
+    }
+    return false;
+  };
+  // keys visible to the whole workgroup (bottom-right causal alignment)
+  auto kv_end_of = [&](const Item& it) {
+    const int wg_qmax = min(it.qb * BQ + BQ, it.Lq) - 1;
+    return CAUSAL ? max(0, min(it.Lk, wg_qmax + 1 + it.Lk - it.Lq)) : it.Lk;
+  };
+  auto rsrc_of = [&](const Item& it, int kv_end) {
+    const u16* base = (k_role ? a.k + (int64_t)it.k_beg * a.k_stride
+                              : a.v + (int64_t)it.k_beg * a.v_stride) + it.h * D;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(base), 0,
+                                             kv_end > 0 ? (kv_end - 1) * row_bytes + D * 2 : 0,
+                                             0x00020000);
+  };
+  // Q fragments: B operand of S^T = K Q^T, lane = query column, 8 dims; rows
+  // past the segment are clamped (and never stored).
+  u32x4 qf[8];
+  f32x16 o[4];  // O^T accumulators (dims 32c..32c+31 x the wave's 32 queries)
+  auto load_q = [&](const Item& it) {
+    const int qi = it.qb * BQ + wq * 32 + col;
+    const int qrow = it.q_beg + min(qi, max(it.Lq - 1, 0));
+    const u16* qp = a.q + (int64_t)qrow * a.q_stride + (it.h * G + wh) * D + hl * 8;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) qf[t] = *reinterpret_cast<const u32x4*>(qp + 16 * t);
+  };
+
+  int k = 0;
+  Item cur;
+  if (!next_item(k, cur)) return;
+  int kv_end = kv_end_of(cur);
+  __amdgpu_buffer_rsrc_t rs = rsrc_of(cur, kv_end);
+
   auto prefetch = [&](int t) {
     const int soff = t * BKV * row_bytes;
 #pragma unroll
@@ -207,11 +243,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   };
   auto stage_write = [&](int t) {
     if (k_role) {
-      u16* ks = Ks[t % STAGES] + k_woff;
+      u16* ks = Ks(t % STAGES) + k_woff;
 #pragma unroll
       for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(ks + 16 * i * KPITCH) = sp[i];
     } else {
-      u16* vt = Vt[t % STAGES];
+      u16* vt = Vt(t % STAGES);
 #pragma unroll
       for (int jw = 0; jw < 4; ++jw) {  // dims st_c+2jw (lo halves) and st_c+2jw+1 (hi halves)
         u32x2 lo, hi;
@@ -226,7 +262,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   };
   // S^T (scores of sub-tile j: keys 32j..32j+31) for this wave's head
   auto scores = [&](int j) {
-    const u16* kr = Ks[(j >> 1) % STAGES] + (j & 1) * 32 * KPITCH + k_rd;
+    const u16* kr = Ks((j >> 1) % STAGES) + (j & 1) * 32 * KPITCH + k_rd;
     f32x16 st;
 #pragma unroll
     for (int i = 0; i < 16; ++i) st[i] = 0.f;
@@ -236,7 +272,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   };
 
   auto pv_step = [&](int jp, const u32x4* pb) {  // O += V(jp) P(jp)
-    const u16* vt = Vt[(jp >> 1) % STAGES] + v_base;
+    const u16* vt = Vt((jp >> 1) % STAGES) + v_base;
     const int g0 = 2 * (jp & 1);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -248,120 +284,236 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
       }
   };
 
-  // Prologue: tile 0 in LDS, tile 1 in flight, S of sub-tile 0.
-  f32x16 sc;
-  if (nt > 0) {
-    prefetch(0);
-    stage_write(0);
-    if (nt > 1) prefetch(1);
-    __syncthreads();
-    sc = scores(0);
-  }
+  // Item prologue (Q and tile 0 in flight): tile 0 in LDS, tile 1 in
+  // flight, S of sub-tile 0.  It is placed before the item loop and at the
+  // end of each iteration, so that each copy waits for exactly its own loads
+  // (one copy at the loop top would merge the wait counts of the first item
+  // with those of later items, which also have the previous item's output
+  // stores outstanding).
+  auto prologue = [&](int nt_) {
+    f32x16 s0;
+    if (nt_ > 0) {
+      stage_write(0);
+      if (nt_ > 1) prefetch(1);
+      __syncthreads();
+      s0 = scores(0);
+    } else {
+      // Q must be complete on this path too: Q left pending on any path into
+      // the tile loop would make every tile wait for all vector loads,
+      // including the prefetch two tiles ahead.  (gfx9 encoding: vmcnt 0,
+      // expcnt and lgkmcnt unconstrained.)
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s0[i] = 0.f;
+    }
+    return s0;
+  };
 
-  // Ring hazard: tile t+1 is written to stage (t+1)%3 after the barrier of
-  // iteration t-1, which every wave reaches only after it has finished all
-  // reads of tile t-2 (the last reader of that stage); the barrier of
-  // iteration t makes tile t+1 visible before the look-ahead scores read it.
-  for (int t = 0; t < nt; ++t) {
-    if (t + 1 < nt) stage_write(t + 1);
-    __syncthreads();
-    if (t + 2 < nt) prefetch(t + 2);
+  load_q(cur);
+  prefetch(0);  // an empty resource (kv_end == 0) reads zeros
+  f32x16 sc = prologue((kv_end + BKV - 1) / BKV);
+
+  for (;;) {
+    // Segment bounds of the next round's item, loaded now so that they have
+    // arrived when this item ends (a dependent load there would cost a
+    // memory round trip per item).  Lane 0 loads the start and lane 1 the
+    // end: a lane-varying load stays in VGPRs until it is used, where a
+    // uniform one would be moved to SGPRs (and waited for) right away.
+    // The loads are issued on every path (segment 0 when there is no
+    // candidate) so that the outstanding-load count the waits below rely on
+    // does not depend on the branch.
+    const int kc = k + 1, ic = item_index(kc);
+    const bool cand = kc * P < n_items && ic < n_items;
+    const int c_sg = (cand ? seg_of(ic) : 0) + (lane & 1);
+    const int c_q = a.cu_q[c_sg];
+    const int c_k = a.cu_k[c_sg];
+
+    const int qi = cur.qb * BQ + wq * 32 + col;  // query index in the segment
+    const int shift = cur.Lk - cur.Lq;  // bottom-right causal alignment
+    // keys visible to this wave / this lane
+    const int w_qmin = cur.qb * BQ + wq * 32;
+    const int w_qmax = min(w_qmin + 31, cur.Lq - 1);
+    const int w_end = w_qmin >= cur.Lq ? 0 : (CAUSAL ? max(0, min(cur.Lk, w_qmax + 1 + shift)) : cur.Lk);
+    const int w_full = CAUSAL ? min(cur.Lk, w_qmin + 1 + shift) : cur.Lk;  // keys < w_full need no mask
+    const int my_lim = CAUSAL ? min(cur.Lk, qi + 1 + shift) : cur.Lk;
+    const int nt = (kv_end + BKV - 1) / BKV;  // LDS tiles (workgroup-uniform)
+    const int nsub = (w_end + 31) / 32;       // 32-key sub-tiles this wave computes
+
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int j = 2 * t + sub;
-      if (j < nsub) {  // wave-uniform
-        // ---- causal mask (only sub-tiles that cross this wave's diagonal)
-        const int kb = 32 * j;
-        if (kb + 32 > w_full) {
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kb + 8 * (i >> 2) + 4 * hl + (i & 3);
-            sc[i] = key < my_lim ? sc[i] : -INFINITY;
+      for (int i = 0; i < 16; ++i) o[c][i] = 0.f;
+    float m = -1e30f, l = 0.f;  // m: reference max of the raw scores (scale applied in exp2)
+
+
+    // Ring hazard: tile t+1 is written to stage (t+1)%3 after the barrier of
+    // iteration t-1, which every wave reaches only after it has finished all
+    // reads of tile t-2 (the last reader of that stage); the barrier of
+    // iteration t makes tile t+1 visible before the look-ahead scores read it.
+    for (int t = 0; t < nt; ++t) {
+      if (t + 1 < nt) stage_write(t + 1);
+      __syncthreads();
+      if (t + 2 < nt) prefetch(t + 2);
+  #pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int j = 2 * t + sub;
+        if (j < nsub) {  // wave-uniform
+          // ---- causal mask (only sub-tiles that cross this wave's diagonal)
+          const int kb = 32 * j;
+          if (kb + 32 > w_full) {
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int key = kb + 8 * (i >> 2) + 4 * hl + (i & 3);
+              sc[i] = key < my_lim ? sc[i] : -INFINITY;
+            }
           }
+          // ---- row max (the partner lane l^32 holds the other 16 keys)
+          float mx = vmax3(sc[0], sc[1], sc[2]);
+  #pragma unroll
+          for (int i = 3; i < 15; i += 2) mx = vmax3(mx, sc[i], sc[i + 1]);
+          mx = vmax(mx, sc[15]);
+          {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                             false, false);
+            mx = vmax(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+          }
+          // Lazy rescaling: the reference max m only moves when some row max
+          // exceeds it by more than kRescale (log2 units), so p <= 2^kRescale
+          // and the accumulators (normalised exactly at the end) are rescaled
+          // rarely; on the first sub-tile they are still zero.
+          if (j == 0) {
+            m = vmax(mx, -1e30f);
+          } else if (__any((mx - m) * a.scale_log2 > kRescale)) {
+            const float mn = vmax(m, mx);
+            const float alpha = fast_exp2((m - mn) * a.scale_log2);
+            m = mn;
+            l *= alpha;
+  #pragma unroll
+            for (int c = 0; c < 4; ++c)
+  #pragma unroll
+              for (int i = 0; i < 16; ++i) o[c][i] *= alpha;
+          }
+          // ---- look-ahead scores of sub-tile j+1 (MFMA) beside the
+          // exponentials of sub-tile j (VALU).  Past the wave's last sub-tile
+          // the look-ahead reads a stale stage and its result is discarded.
+          const float nb = -m * a.scale_log2;
+          const f32x16 sn = scores(j + 1);
+          float p[16];
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sc[i], a.scale_log2, nb));
+          u32x4 pb[2];
+  #pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+  #pragma unroll
+            for (int w = 0; w < 4; ++w) pb[tt][w] = M::pack(p[8 * tt + 2 * w], p[8 * tt + 2 * w + 1]);
+          // row sum of the rounded probabilities the PV product uses
+  #pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+  #pragma unroll
+            for (int w = 0; w < 4; ++w) l = M::dot2_ones(pb[tt][w], l);
+          pv_step(j, pb);
+          sc = sn;
         }
-        // ---- row max (the partner lane l^32 holds the other 16 keys)
-        float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
-#pragma unroll
-        for (int i = 3; i < 15; i += 2) mx = fmaxf(mx, fmaxf(sc[i], sc[i + 1]));
-        mx = fmaxf(mx, sc[15]);
-        {
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
-                                                           false, false);
-          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        // Lazy rescaling: the reference max m only moves when some row max
-        // exceeds it by more than kRescale (log2 units), so p <= 2^kRescale
-        // and the accumulators (normalised exactly at the end) are rescaled
-        // rarely; on the first sub-tile they are still zero.
-        if (j == 0) {
-          m = fmaxf(mx, -1e30f);
-        } else if (__any((mx - m) * a.scale_log2 > kRescale)) {
-          const float mn = fmaxf(m, mx);
-          const float alpha = fast_exp2((m - mn) * a.scale_log2);
-          m = mn;
-          l *= alpha;
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[c][i] *= alpha;
-        }
-        // ---- look-ahead scores of sub-tile j+1 (MFMA) beside the
-        // exponentials of sub-tile j (VALU).  Past the wave's last sub-tile
-        // the look-ahead reads a stale stage and its result is discarded.
-        const float nb = -m * a.scale_log2;
-        const f32x16 sn = scores(j + 1);
-        float p[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sc[i], a.scale_log2, nb));
-        u32x4 pb[2];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) pb[tt][w] = M::pack(p[8 * tt + 2 * w], p[8 * tt + 2 * w + 1]);
-        // row sum of the rounded probabilities the PV product uses
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) l = M::dot2_ones(pb[tt][w], l);
-        pv_step(j, pb);
-        sc = sn;
       }
     }
-  }
 
-  // ---- epilogue: full row sum (partner lane holds the other 16 keys of each
-  // 32-key sub-tile), normalise, store.
-  if (!q_ok) return;
-  const float lt = l + __shfl_xor(l, 32);
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  u16* op = a.out + (int64_t)(q_beg + qi) * a.o_stride + (h * G + wh) * D + 4 * hl;
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      u32x2 w;
-      w[0] = M::pack(o[c][4 * r] * inv, o[c][4 * r + 1] * inv);
-      w[1] = M::pack(o[c][4 * r + 2] * inv, o[c][4 * r + 3] * inv);
-      *reinterpret_cast<u32x2*>(op + 32 * c + 8 * r) = w;
+    // The next item's Q and first K/V tile go out before this item's
+    // epilogue, so their latency overlaps the normalisation and stores.
+    Item nxt;
+    int kn = kc;
+    bool more;
+    if (cand && decode(ic, __builtin_amdgcn_readlane(c_q, 0), __builtin_amdgcn_readlane(c_q, 1),
+                       __builtin_amdgcn_readlane(c_k, 0), __builtin_amdgcn_readlane(c_k, 1), nxt)) {
+      more = true;
+    } else {  // a hole or a missing rank: search the later rounds
+      kn = kc + 1;
+      more = kc * P < n_items && next_item(kn, nxt);
     }
+    if (more) {
+      kv_end = kv_end_of(nxt);
+      rs = rsrc_of(nxt, kv_end);
+      load_q(nxt);
+      prefetch(0);
+    }
+
+    // ---- epilogue: full row sum (partner lane holds the other 16 keys of
+    // each 32-key sub-tile), normalise, store.  The tile goes through LDS so
+    // that each store instruction writes four whole 256-byte head rows (the
+    // accumulator layout would scatter 8-byte pieces over 32 rows per store).
+    const float lt = l + __shfl_xor(l, 32);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    __syncthreads();  // every wave is done with the ring (including the discarded look-ahead)
+    u16* ob = lds + wave * (32 * OPITCH);  // this wave's 32 rows x 128 dims
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        u32x2 wv;
+        wv[0] = M::pack(o[c][4 * r] * inv, o[c][4 * r + 1] * inv);
+        wv[1] = M::pack(o[c][4 * r + 2] * inv, o[c][4 * r + 3] * inv);
+        *reinterpret_cast<u32x2*>(ob + col * OPITCH + 32 * c + 8 * r + 4 * hl) = wv;
+      }
+    {
+      const int row0 = cur.qb * BQ + wq * 32;  // the wave's first query
+      u16* og = a.out + (int64_t)(cur.q_beg + row0) * a.o_stride + (cur.h * G + wh) * D + (lane & 15) * 8;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int r = 4 * it + (lane >> 4);
+        const u32x4 val = *reinterpret_cast<const u32x4*>(ob + r * OPITCH + (lane & 15) * 8);
+        if (row0 + r < cur.Lq) *reinterpret_cast<u32x4*>(og + (int64_t)r * a.o_stride) = val;
+      }
+    }
+    if (!more) break;
+    // Every wave has read its output rows back before the next item's tile 0
+    // overwrites them.
+    __syncthreads();
+    cur = nxt;
+    k = kn;
+    sc = prologue((kv_end + BKV - 1) / BKV);
+  }
 }
 
 template <int G, bool CAUSAL, bool F16>
-static void launch_t(const Args& a, int max_q, hipStream_t st) {
+static void launch_t(Args a, int max_q, int n_cu, hipStream_t st) {
   constexpr int BQ = 32 * (kWaves / G);
-  dim3 grid(a.hkv, a.n_seqs, (unsigned)cdiv(max_q, BQ));
-  hipLaunchKernelGGL((prefill_kernel<G, CAUSAL, F16>), grid, dim3(kThreads), 0, st, a);
+  a.n_qblocks = (int)cdiv(max_q, BQ);
+  const int64_t n_items = (int64_t)a.hkv * a.n_seqs * a.n_qblocks;
+  const int grid = (int)std::min<int64_t>(n_items, n_cu);  // persistent: one workgroup per CU
+  hipLaunchKernelGGL((prefill_kernel<G, CAUSAL, F16>), dim3(grid), dim3(kThreads), 0, st, a);
 }
 
 template <bool CAUSAL, bool F16>
-static int launch_g(const Args& a, int g, int max_q, hipStream_t st) {
+static int launch_g(const Args& a, int g, int max_q, int n_cu, hipStream_t st) {
   switch (g) {
-    case 1: launch_t<1, CAUSAL, F16>(a, max_q, st); break;
-    case 2: launch_t<2, CAUSAL, F16>(a, max_q, st); break;
-    case 4: launch_t<4, CAUSAL, F16>(a, max_q, st); break;
-    case 8: launch_t<8, CAUSAL, F16>(a, max_q, st); break;
+    case 1: launch_t<1, CAUSAL, F16>(a, max_q, n_cu, st); break;
+    case 2: launch_t<2, CAUSAL, F16>(a, max_q, n_cu, st); break;
+    case 4: launch_t<4, CAUSAL, F16>(a, max_q, n_cu, st); break;
+    case 8: launch_t<8, CAUSAL, F16>(a, max_q, n_cu, st); break;
     default: return AAC_ERR_UNSUPPORTED;
   }
+  return AAC_OK;
+}
+
+// Compute units of the current device (the persistent grid size), cached per
+// device; a racing first query stores the same value twice.
+static int device_cu_count(int* n_cu) {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *n_cu = c;
+      return AAC_OK;
+    }
+  }
+  int n = 0;
+  e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return (int)e;
+  if (n <= 0) return AAC_ERR_UNSUPPORTED;
+  if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  *n_cu = n;
   return AAC_OK;
 }
 
@@ -394,6 +546,9 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
   // staging uses 32-bit byte offsets within one segment's K/V rows
   if ((int64_t)max_seqlen_k * std::max(k_tok_stride, v_tok_stride) * 2 >= (int64_t(1) << 31))
     return AAC_ERR_UNSUPPORTED;
+  // work items (KV head, segment, 32-query block at most) are numbered in int32
+  if ((int64_t)n_kv_heads * n_seqs * cdiv(max_seqlen_q, 32) >= (int64_t(1) << 30))
+    return AAC_ERR_UNSUPPORTED;
   if (!launch) return AAC_OK;
   pf::Args a;
   a.q = (const u16*)q;
@@ -411,13 +566,15 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
   a.scale_log2 = scale * kLog2e;
   a.out = (u16*)out;
   const bool f16 = dtype == AAC_DTYPE_FP16;
-  int rc;
+  int n_cu = 0;
+  int rc = pf::device_cu_count(&n_cu);
+  if (rc != AAC_OK) return rc;
   if (causal)
-    rc = f16 ? pf::launch_g<true, true>(a, g, max_seqlen_q, stream)
-             : pf::launch_g<true, false>(a, g, max_seqlen_q, stream);
+    rc = f16 ? pf::launch_g<true, true>(a, g, max_seqlen_q, n_cu, stream)
+             : pf::launch_g<true, false>(a, g, max_seqlen_q, n_cu, stream);
   else
-    rc = f16 ? pf::launch_g<false, true>(a, g, max_seqlen_q, stream)
-             : pf::launch_g<false, false>(a, g, max_seqlen_q, stream);
+    rc = f16 ? pf::launch_g<false, true>(a, g, max_seqlen_q, n_cu, stream)
+             : pf::launch_g<false, false>(a, g, max_seqlen_q, n_cu, stream);
   if (rc != AAC_OK) return rc;
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? AAC_OK : (int)e;
