@@ -64,6 +64,17 @@ template <> struct Elem<Dt::BF16> {
     }
   }
   __device__ static inline u32 pack2(float a, float b) { return pack_bf16x2(a, b); }
+  // hardware round-to-nearest-even pack (v_cvt_pk_bf16_f32)
+  __device__ static inline u32 pack2_hw(float a, float b) {
+    typedef __attribute__((ext_vector_type(2))) float f2;
+    return __builtin_bit_cast(u32, __builtin_convertvector((f2){a, b}, bf16x2));
+  }
+  // acc + x.lo * y.lo + x.hi * y.hi in fp32 (v_dot2_f32_bf16)
+  __device__ static inline float dot2(u32 x, u32 y, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), __builtin_bit_cast(bf16x2, y),
+                                           acc, false);
+  }
+  static constexpr u32 kOnes = 0x3f803f80u;  // (1.0, 1.0)
 };
 template <> struct Elem<Dt::FP16> {
   static constexpr int kBytes = 2;
@@ -75,10 +86,21 @@ template <> struct Elem<Dt::FP16> {
     }
   }
   __device__ static inline u32 pack2(float a, float b) { return pack_f16x2(a, b); }
+  __device__ static inline u32 pack2_hw(float a, float b) { return pack_f16x2(a, b); }
+  // acc + x.lo * y.lo + x.hi * y.hi in fp32 (v_dot2_f32_f16)
+  __device__ static inline float dot2(u32 x, u32 y, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), __builtin_bit_cast(f16x2, y), acc,
+                                  false);
+  }
+  static constexpr u32 kOnes = 0x3c003c00u;  // (1.0, 1.0)
 };
 template <> struct Elem<Dt::FP32> {
   static constexpr int kBytes = 4;
 };
+
+// byte-select masks for v_perm_b32(hi_src, lo_src, sel) on 16-bit pairs
+constexpr u32 kSelLo = 0x05040100u;  // (lo16 of lo_src, lo16 of hi_src)
+constexpr u32 kSelHi = 0x07060302u;  // (hi16 of lo_src, hi16 of hi_src)
 
 // ---------------------------------------------------------------- DPP
 // dpp_ctrl encodings (GCN/CDNA DPP16)

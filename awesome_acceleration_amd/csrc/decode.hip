@@ -139,8 +139,12 @@ __global__ __launch_bounds__(256) void decode_paged_kernel(DecodeArgs a) {
   const int li = lane & 15, grp = lane >> 4;
   const int rslot = wave * 4 + grp;  // 0..15
 
-  // q for the G heads of this KV head, pre-scaled into the log2 domain.
-  float qf[G][8];
+  // q for the G heads of this KV head.  fp32: unpacked and pre-scaled into
+  // the log2 domain.  bf16/fp16 (PK): kept packed and exact for v_dot2; the
+  // scale is applied to the scores instead.
+  constexpr bool PK = DT != Dt::FP32;
+  float qf[PK ? 1 : G][8];
+  u32 qp[PK ? G : 1][4];
   {
     const char* qb = reinterpret_cast<const char*>(a.q) +
                      ((int64_t)b * a.q_seq_stride + (int64_t)h * G * kHeadDim + li * 8) * ES;
@@ -148,9 +152,14 @@ __global__ __launch_bounds__(256) void decode_paged_kernel(DecodeArgs a) {
     for (int g = 0; g < G; ++g) {
       Raw8<DT> r;
       r.load(qb + (int64_t)g * kHeadDim * ES);
-      r.unpack(qf[g]);
+      if constexpr (PK) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qf[g][i] *= a.scale_log2;
+        for (int w = 0; w < 4; ++w) qp[g][w] = r.w[0][w];
+      } else {
+        r.unpack(qf[g]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[g][i] *= a.scale_log2;
+      }
     }
   }
 
@@ -163,67 +172,132 @@ __global__ __launch_bounds__(256) void decode_paged_kernel(DecodeArgs a) {
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
   }
 
-  const int64_t tok_elems = (int64_t)a.hkv * kHeadDim;  // cache row stride (elements)
+  const int64_t tok_bytes = (int64_t)a.hkv * kHeadDim * ES;  // cache row stride
   const char* kbase = reinterpret_cast<const char*>(a.k_cache) + ((int64_t)h * kHeadDim + li * 8) * ES;
   const char* vbase = reinterpret_cast<const char*>(a.v_cache) + ((int64_t)h * kHeadDim + li * 8) * ES;
   const int32_t* bt = a.block_tables + (int64_t)b * a.max_blocks;
+  const uint32_t nb32 = a.num_blocks < 0x7fffffff ? (uint32_t)a.num_blocks : 0x7fffffffu;
+
+  // Token t of this partition, or t0 (a valid token whose row is finite and
+  // whose probability is set to 0) past its end, so loads never branch.
+  auto token = [&](int t) { return t < t1 ? t : t0; };
+  auto block_index = [&](int t) { return POW2 ? t >> a.bs_shift : t / a.block_size; };
+  // The block numbers of an iteration's U tokens are loaded one iteration
+  // ahead: a block-table load waited for right before the K/V loads would,
+  // with in-order load counters, also wait for every K/V load issued before
+  // it and leave one token per wave in flight.
+  int blk[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) blk[u] = bt[block_index(token(t0 + rslot + 16 * u))];
 
   for (int tb = t0 + rslot; tb < t1; tb += 16 * U) {
     Raw8<DT> kr[U], vr[U];
     bool valid[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t = tb + 16 * u;
-      valid[u] = t < t1;
-      if (valid[u]) {
-        const int bi = POW2 ? t >> a.bs_shift : t / a.block_size;
-        int blk = bt[bi];
-        if (blk < 0 || blk >= a.num_blocks) blk = 0;
-        const int off = POW2 ? t & (a.block_size - 1) : t - bi * a.block_size;
-        const int64_t row = (int64_t)blk * a.block_size + off;
-        kr[u].load(kbase + row * tok_elems * ES);
-        vr[u].load(vbase + row * tok_elems * ES);
-      } else {
-        kr[u].zero();
-        vr[u].zero();
-      }
+      valid[u] = tb + 16 * u < t1;
+      const int t = token(tb + 16 * u);
+      const int bi = block_index(t);
+      const int off = POW2 ? t & (a.block_size - 1) : t - bi * a.block_size;
+      const uint32_t bk = (uint32_t)blk[u] < nb32 ? (uint32_t)blk[u] : 0u;  // bad entries read block 0
+      const int64_t row = (int64_t)bk * a.block_size + off;
+      kr[u].load(kbase + row * tok_bytes);
+      vr[u].load(vbase + row * tok_bytes);
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) blk[u] = bt[block_index(token(tb + 16 * U + 16 * u))];
+    // Every load above is issued before any arithmetic below (the scheduler
+    // would otherwise pull each token's math up behind its load and wait).
+    __builtin_amdgcn_sched_barrier(0);
     float s[U][G];
+    if constexpr (PK) {
+      // Packed bf16/fp16: q.k with v_dot2 on the packed rows (no unpacking),
+      // raw scores; the probabilities are rounded to the input type (as the
+      // MFMA prefill and FA2 do for the PV product) and packed per token pair,
+      // so that P V is v_dot2 too, over V words paired across two tokens by
+      // v_perm.  The row sum l adds the same rounded probabilities.
+      typedef Elem<DT> E;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float kf[8];
-      kr[u].unpack(kf);
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float d = 0.f;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) d = E::dot2(kr[u].w[0][w], qp[g][w], d);
+          d = row16_sum(d);
+          s[u][g] = valid[u] ? d : -INFINITY;
+        }
+      u32 pp[U / 2][G];
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float d = 0.f;
+        float mr = s[0][g];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
-        d = row16_sum(d);
-        s[u][g] = valid[u] ? d : -INFINITY;
+        for (int u = 1; u + 1 < U; u += 2) mr = vmax3(mr, s[u][g], s[u + 1][g]);
+        mr = vmax(mr, s[U - 1][g]);
+        const float mx = vmax(m[g], mr * a.scale_log2);
+        const float alpha = fast_exp2(m[g] - mx);
+        m[g] = mx;
+        l[g] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+#pragma unroll
+        for (int v = 0; v < U / 2; ++v) {
+          const float p0 = fast_exp2(fmaf(s[2 * v][g], a.scale_log2, -mx));
+          const float p1 = fast_exp2(fmaf(s[2 * v + 1][g], a.scale_log2, -mx));
+          pp[v][g] = E::pack2_hw(p0, p1);
+          l[g] = E::dot2(pp[v][g], E::kOnes, l[g]);
+        }
       }
-    }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mx = m[g];
+      for (int v = 0; v < U / 2; ++v)
 #pragma unroll
-      for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][g]);
-      const float alpha = fast_exp2(m[g] - mx);
-      m[g] = mx;
-      l[g] *= alpha;
+        for (int w = 0; w < 4; ++w) {
+          // (token 2v, token 2v+1) of dims 2w and 2w+1
+          const u32 lo = __builtin_amdgcn_perm(vr[2 * v + 1].w[0][w], vr[2 * v].w[0][w], kSelLo);
+          const u32 hi = __builtin_amdgcn_perm(vr[2 * v + 1].w[0][w], vr[2 * v].w[0][w], kSelHi);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+          for (int g = 0; g < G; ++g) {
+            acc[g][2 * w] = E::dot2(lo, pp[v][g], acc[g][2 * w]);
+            acc[g][2 * w + 1] = E::dot2(hi, pp[v][g], acc[g][2 * w + 1]);
+          }
+        }
+    } else {
 #pragma unroll
-      for (int u = 0; u < U; ++u) s[u][g] = fast_exp2(s[u][g] - mx);
-    }
+      for (int u = 0; u < U; ++u) {
+        float kf[8];
+        kr[u].unpack(kf);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float vf[8];
-      vr[u].unpack(vf);
+        for (int g = 0; g < G; ++g) {
+          float d = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
+          d = row16_sum(d);
+          s[u][g] = valid[u] ? d : -INFINITY;
+        }
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        l[g] += s[u][g];
+        float mx = m[g];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(s[u][g], vf[i], acc[g][i]);
+        for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][g]);
+        const float alpha = fast_exp2(m[g] - mx);
+        m[g] = mx;
+        l[g] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+#pragma unroll
+        for (int u = 0; u < U; ++u) s[u][g] = fast_exp2(s[u][g] - mx);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float vf[8];
+        vr[u].unpack(vf);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          l[g] += s[u][g];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(s[u][g], vf[i], acc[g][i]);
+        }
       }
     }
   }
@@ -330,13 +404,14 @@ static DecodePlan plan_decode(int32_t n_seqs, int32_t hq, int32_t hkv, int32_t b
   if (part <= 0) {
     // Measured on MI355X (bf16, block 256): with >= 1024 (sequence, KV head)
     // items and contexts up to 4096 tokens one workgroup per item streams at
-    // the HBM ceiling and needs no reduction; otherwise 1024-token partitions,
-    // shrunk (down to 256) until there are >= 2048 workgroups for 256 CUs.
+    // the HBM ceiling and needs no reduction; otherwise 2048-token partitions
+    // (64 x 16k-32k GQA-4: 2048 beats 1024 by 3%), halved (down to 256) until
+    // there are >= 2048 workgroups for 256 CUs.
     const int64_t items = (int64_t)n_seqs * hkv;
     if (items >= 1024 && cap <= 4096) {
       part = cap;
     } else {
-      part = 1024;
+      part = 2048;
       while (part > 256 && items * cdiv(cap, part) < 2048) part /= 2;
     }
   }

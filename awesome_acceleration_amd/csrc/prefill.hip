@@ -93,9 +93,6 @@ template <> struct Mfma<true> {
   }
 };
 
-// byte-select masks for v_perm_b32(hi_src, lo_src, sel)
-constexpr u32 kSelLo = 0x05040100u;  // (lo16 of lo_src, lo16 of hi_src)
-constexpr u32 kSelHi = 0x07060302u;  // (hi16 of lo_src, hi16 of hi_src)
 
 // V^T tile layout: 128 rows (dims) x 64 keys, no padding.  Keys are handled
 // in quads (4 keys = 8 bytes).  Inside each 16-key group the quad order is

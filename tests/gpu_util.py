@@ -43,7 +43,7 @@ def check_attention(out: torch.Tensor, ref: np.ndarray, atol: float = ATOL_BF16,
     * Output rounding: at most 2^-9 |ref| for a bf16 result.
     * ``absv`` (optional) is the same attention evaluated with |V|, i.e.
       sum_j p_j |v_j|.  When the kernel rounds the probabilities to bf16 before
-      the PV product (as the MFMA prefill does, like FA2), each term carries at
+      the PV product (as the MFMA prefill and the bf16/fp16 decode do, like FA2), each term carries at
       most 2^-9 relative error, so the sum moves by at most 2^-9 * absv.
     Both bounds get a factor 2 of margin for fp32 accumulation and exp2
     approximation error, plus a small absolute floor.

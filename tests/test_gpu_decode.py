@@ -23,6 +23,13 @@ GOLD = Path(__file__).resolve().parent / "golden"
 MANIFEST = json.loads((GOLD / "manifest.json").read_text())
 
 
+def _abs_v(x):
+    """|x| for bf16 bit patterns (sign bit cleared) or float arrays: the V of
+    the attention sum_j p_j |v_j| that bounds the effect of rounding the
+    probabilities to bf16/fp16 before the PV product."""
+    return x & np.uint16(0x7FFF) if x.dtype == np.uint16 else np.abs(x)
+
+
 def _run_fixture(inp, gpu, dtype):
     q = t_of(inp["q"], gpu, dtype)
     kc = t_of(inp["k_cache"], gpu, dtype)
@@ -59,7 +66,10 @@ def test_tiny_bf16_fixture(gpu):
     man = MANIFEST["tiny_decode_bf16"]
     assert sha256(np_of(kc)) == man["digest_k_cache_after"]
     assert sha256(np_of(vc)) == man["digest_v_cache_after"]
-    check_attention(out, fx["out"], what="tiny bf16")
+    absv, _ = oracle.decode_append_attend(inp["q"], inp["k_cache"].copy(), _abs_v(inp["v_cache"]),
+                                          inp["k_new"], _abs_v(inp["v_new"]), inp["block_tables"],
+                                          inp["cache_seqlens"], inp["block_size"], inp["scale"])
+    check_attention(out, fx["out"], what="tiny bf16", absv=absv)
 
 
 def _random_paged(B, hq, hkv, ctx, bs, seed, gpu, dtype=torch.bfloat16, extra_blocks=3):
@@ -83,7 +93,7 @@ def _random_paged(B, hq, hkv, ctx, bs, seed, gpu, dtype=torch.bfloat16, extra_bl
     return q, kc, vc, kn, vn, bt
 
 
-def _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, seqs, scale):
+def _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, seqs, scale, abs_v=False):
     out = {}
     for b in seqs:
         ks = oracle.gather_paged(kc_np, bt[b], int(ctx[b]), bs)
@@ -92,6 +102,8 @@ def _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, seqs, scale):
             ks, vs, qb = bf16_np_to_f64(ks), bf16_np_to_f64(vs), bf16_np_to_f64(q_np[b])
         else:
             ks, vs, qb = ks.astype(np.float64), vs.astype(np.float64), q_np[b].astype(np.float64)
+        if abs_v:
+            vs = np.abs(vs)
         out[b] = oracle.paged_decode(qb[None], ks[None], vs[None],
                                      np.arange(1, dtype=np.int32)[None], [int(ctx[b])],
                                      block_size=int(ctx[b]), scale=scale)[0]
@@ -119,8 +131,9 @@ def test_decode_256_seqs_full_size(gpu):
     assert np.array_equal(kc_np.reshape(-1, hkv, 128)[sm], np_of(kn))
     assert np.array_equal(vc_np.reshape(-1, hkv, 128)[sm], np_of(vn))
     ref = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), scale)
+    absv = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), scale, abs_v=True)
     check_attention(out.view(B, hq, 128), np.stack([ref[b] for b in range(B)]),
-                    what="decode 256 seqs")
+                    what="decode 256 seqs", absv=np.stack([absv[b] for b in range(B)]))
 
 
 def test_decode_long_context_gqa4_sampled(gpu):
@@ -151,9 +164,9 @@ def test_decode_long_context_gqa4_sampled(gpu):
     vc_np = np_of(vc[torch.from_numpy(used.astype(np.int64)).to(gpu)])
     bt_local = np.vectorize(lambda x: remap[int(x)])(bt_s).astype(np.int32)
     for i, b in enumerate(sample):
-        ref = _oracle_rows(kc_np, vc_np, q_np[b:b + 1], bt_local[i:i + 1], ctx[b:b + 1], bs, [0],
-                           scale)[0]
-        check_attention(out[b], ref, what=f"long ctx seq {b}")
+        rows = (kc_np, vc_np, q_np[b:b + 1], bt_local[i:i + 1], ctx[b:b + 1], bs, [0], scale)
+        check_attention(out[b], _oracle_rows(*rows)[0], what=f"long ctx seq {b}",
+                        absv=_oracle_rows(*rows, abs_v=True)[0])
 
 
 def test_reference_slot_layout_via_cache_batch_idx(gpu):
@@ -184,7 +197,11 @@ def test_reference_slot_layout_via_cache_batch_idx(gpu):
         np_of(v.contiguous()).reshape(B, hkv, 128), bt, seqlens.cpu().numpy(), lmax, 128 ** -0.5)
     assert np.array_equal(np_of(kc), kc_before)  # oracle stored into kc_before in place
     assert np.array_equal(np_of(vc), vc_before)
-    check_attention(out.view(B, hq, 128), ref, what="slot layout")
+    absv, _ = oracle.decode_append_attend(
+        np_of(q).reshape(B, hq, 128), kc_before, _abs_v(vc_before),
+        np_of(k.contiguous()).reshape(B, hkv, 128), _abs_v(np_of(v.contiguous()).reshape(B, hkv, 128)),
+        bt, seqlens.cpu().numpy(), lmax, 128 ** -0.5)
+    check_attention(out.view(B, hq, 128), ref, what="slot layout", absv=absv)
 
 
 @pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
@@ -201,7 +218,9 @@ def test_decode_gqa_groups_and_dtypes(gpu, hq, hkv, dtype):
         kc_np, vc_np = f64(kc), f64(vc)
         q_np = f64(q)
         ref = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), 0.1)
-        check_attention(out, np.stack([ref[b] for b in range(B)]), what=f"gqa part={part}")
+        absv = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), 0.1, abs_v=True)
+        check_attention(out, np.stack([ref[b] for b in range(B)]), what=f"gqa part={part}",
+                        absv=np.stack([absv[b] for b in range(B)]))
 
 
 def test_decode_edge_cases_and_block_relabelling(gpu):
