@@ -13,6 +13,9 @@ inputs resident in HBM.
 Also reported on the same line:
   roofline      the decode attention launch alone (aac_decode_paged), timed
                 with HIP events on the launch stream, against 8 TB/s HBM;
+  decode_long   long-context GQA-4 decode (64 sequences, 32 query / 8 KV heads,
+                context ~ U[16384, 32768]): the split-K decode plus its
+                log-sum-exp reduction, HIP events, against 8 TB/s HBM;
   prefill       varlen causal prefill, 8 x 1024 tokens, 16/8 heads, bf16, with
                 the paged store in the same call, as TFLOP/s against the
                 2.5 PFLOP/s dense bf16 MFMA peak (roofline of that kernel);
@@ -64,11 +67,12 @@ def parse():
     p.add_argument("--partition", type=int, default=0, help="decode partition tokens (0=auto)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-long", action="store_true", help="skip the long-context GQA-4 decode leg")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine leg")
     p.add_argument("--e2e-seqs", type=int, default=256)
     p.add_argument("--e2e-in", type=int, default=1024)
     p.add_argument("--e2e-out", type=int, default=1024)
-    p.add_argument("--only", choices=["decode", "prefill", "e2e"], default=None,
+    p.add_argument("--only", choices=["decode", "decode_long", "prefill", "e2e"], default=None,
                    help="run one leg only (for profiling)")
     return p.parse_args()
 
@@ -76,9 +80,10 @@ def parse():
 # ----------------------------------------------------------------------------
 # decode: 256 seqs x ctx U[1024, 2047]
 # ----------------------------------------------------------------------------
-def make_decode_inputs(torch, dev, seed, B=256, hq=16, hkv=8, d=128, bs=256):
+def make_decode_inputs(torch, dev, seed, B=256, hq=16, hkv=8, d=128, bs=256, ctx_lo=1024,
+                       ctx_hi=2048):
     rs = np.random.RandomState(seed)
-    ctx = rs.randint(1024, 2048, B).astype(np.int32)          # after the store
+    ctx = rs.randint(ctx_lo, ctx_hi, B).astype(np.int32)      # after the store
     need = [int(-(-c // bs)) for c in ctx]
     pool = sum(need)
     perm = rs.permutation(pool).astype(np.int32)
@@ -150,6 +155,44 @@ def bench_decode(torch, fai, dev, args):
     return dict(
         t_step=t_step, step_bytes=step_bytes, attend_bytes=attend_bytes, t_attend=t_att,
         achieved=achieved, x=x)
+
+
+# ----------------------------------------------------------------------------
+# long-context GQA-4 decode: 64 seqs x ctx U[16384, 32768], 32/8 heads (split-K)
+# ----------------------------------------------------------------------------
+def bench_decode_long(torch, fai, dev, args):
+    x = make_decode_inputs(torch, dev, args.seed, B=64, hq=32, hkv=8, ctx_lo=16384,
+                           ctx_hi=32769)
+    attend_bytes, _ = decode_bytes(x)
+    maxctx = int(x["ctx"].max())
+    q3 = x["q"].view(x["B"], x["hq"], x["d"])
+    out3 = torch.empty_like(q3)
+
+    def attend():  # the decode kernel plus the split-K reduction
+        return fai.decode_paged(q3, x["kc"], x["vc"], x["bt_g"], x["ctx_g"],
+                                max_context_len=maxctx, out=out3)
+
+    for _ in range(args.warmup):
+        attend()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for a, b in evs:
+        a.record()
+        attend()
+        b.record()
+    torch.cuda.synchronize()
+    t = sum(a.elapsed_time(b) for a, b in evs) / len(evs) / 1e3
+    ach = attend_bytes / t / 1e9
+    return {
+        "workload": "paged decode attend, 64 seqs, 32 q / 8 kv heads (GQA-4), head_dim 128, "
+                    "context U[16384,32768], block 256, split-K with log-sum-exp reduction (auto plan)",
+        "context_tokens": int(x["ctx"].sum()),
+        "us_per_call": round(t * 1e6, 2),
+        "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "bytes_per_call": attend_bytes,
+                     "traffic": None},
+    }
 
 
 # ----------------------------------------------------------------------------
@@ -290,6 +333,9 @@ def main():
     res = {}
     if args.only in (None, "decode"):
         res["decode"] = bench_decode(torch, fai, dev, args)
+    if args.only in (None, "decode_long") and not args.no_long:
+        res["decode_long"] = bench_decode_long(torch, fai, dev, args)
+        torch.cuda.empty_cache()
     if args.only in (None, "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, fai, paged, dev, args)
     if args.only in (None, "e2e") and not args.no_e2e:
@@ -351,6 +397,8 @@ def main():
                          "frac": round(pf["tflops"] / BF16_PEAK_TFLOPS, 4),
                          "flops_per_launch": pf["flops"], "traffic": None},
         }
+    if "decode_long" in res:
+        line["decode_long"] = res["decode_long"]
     if "e2e" in res:
         line["e2e"] = res["e2e"]
     if not args.no_cpu:
