@@ -1,0 +1,146 @@
+// KV export / import between the paged cache and one contiguous buffer -- the
+// reference's export_kv / import_kv (model/model.py:156-177) and
+// export_request_kv / import_request_kv (model/model.py:386-401): the
+// prefill->decode migration payload {"layers": [{"k", "v", "seqlen"}]} that
+// pd/kv_connector_shm.py:97-151 ships between processes.
+//
+// The reference slices cache[slot, :length] per layer and copies each slice
+// to the host separately (2 x 28 device->host copies per request).  Here one
+// launch gathers every layer's K and V rows of a sequence, through its block
+// table, into a contiguous [n_layers][2][length][Hkv*D] buffer (so the host
+// transfer is one copy), and the import scatters such a buffer back into
+// whichever blocks the receiving side allocated.
+//
+// Work decomposition: grid = (ceil(length / 4), 2 * n_layers); each of the 4
+// wavefronts of a workgroup moves one token row (Hkv * D * elem bytes, 2 KiB
+// for Qwen3 bf16) of one layer's K or V with 16-byte accesses, all loads of a
+// lane before its stores.  Pure data movement: HBM-bound, 2 * row bytes per
+// (layer, K/V, token) moved (read + write).
+//
+// Block-table entries outside [0, num_blocks) export zeros and are never
+// written by the import (as the KV store skips invalid slots).
+
+#include "aac_common.h"
+
+namespace aac {
+
+namespace {
+
+struct XferArgs {
+  char* cache;           // layer 0 K cache (bytes)
+  int64_t layer_stride;  // bytes between consecutive layers' caches
+  int64_t kv_stride;     // bytes from a layer's K cache to its V cache
+  int64_t num_blocks;
+  int32_t block_size;
+  const int32_t* block_table;
+  int32_t length;
+  int32_t row_chunks;  // 16-byte chunks per token row
+  char* buf;           // [n_layers][2][length][row]
+};
+
+constexpr int kChunksPerLane = 4;  // up to 4 x 64 x 16 B = 4 KiB rows in registers
+
+template <bool EXPORT>
+__global__ __launch_bounds__(256) void kv_xfer_kernel(XferArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= a.length) return;
+  const int lc = blockIdx.y;  // layer * 2 + (0: K, 1: V)
+  const int64_t row_bytes = (int64_t)a.row_chunks * 16;
+  const int bi = t / a.block_size;
+  const int32_t blk = a.block_table[bi];
+  const bool ok = blk >= 0 && blk < a.num_blocks;
+  char* crow = a.cache + (int64_t)(lc >> 1) * a.layer_stride + (int64_t)(lc & 1) * a.kv_stride +
+               ((int64_t)blk * a.block_size + (t - bi * a.block_size)) * row_bytes;
+  char* brow = a.buf + ((int64_t)lc * a.length + t) * row_bytes;
+  for (int c0 = 0; c0 < a.row_chunks; c0 += 64 * kChunksPerLane) {
+    u32x4 v[kChunksPerLane];
+#pragma unroll
+    for (int i = 0; i < kChunksPerLane; ++i) {
+      const int c = c0 + i * 64 + lane;
+      v[i] = u32x4{0, 0, 0, 0};
+      if (c < a.row_chunks) {
+        if (EXPORT) {
+          if (ok) v[i] = *reinterpret_cast<const u32x4*>(crow + c * 16);
+        } else {
+          v[i] = *reinterpret_cast<const u32x4*>(brow + c * 16);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kChunksPerLane; ++i) {
+      const int c = c0 + i * 64 + lane;
+      if (c < a.row_chunks) {
+        if (EXPORT)
+          *reinterpret_cast<u32x4*>(brow + c * 16) = v[i];
+        else if (ok)
+          *reinterpret_cast<u32x4*>(crow + c * 16) = v[i];
+      }
+    }
+  }
+}
+
+int xfer(bool export_, const void* cache, int64_t layer_stride, int64_t kv_stride, int32_t n_layers,
+         int64_t num_blocks, int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
+         const int32_t* block_table, int32_t max_blocks, int32_t length, void* buf, int32_t dtype,
+         void* stream) {
+  int es;
+  switch (dtype) {
+    case AAC_DTYPE_BF16:
+    case AAC_DTYPE_FP16: es = 2; break;
+    case AAC_DTYPE_FP32: es = 4; break;
+    default: return AAC_ERR_UNSUPPORTED;
+  }
+  if (n_layers < 0 || length < 0 || block_size <= 0 || n_kv_heads <= 0 || head_dim <= 0 ||
+      num_blocks < 0 || max_blocks < 0)
+    return AAC_ERR_INVALID_ARGUMENT;
+  if ((int64_t)length > (int64_t)max_blocks * block_size) return AAC_ERR_SHAPE;
+  if (n_layers == 0 || length == 0) return AAC_OK;
+  if (!cache || !buf || !block_table) return AAC_ERR_INVALID_ARGUMENT;
+  if (n_layers > 32768) return AAC_ERR_UNSUPPORTED;  // grid.y = 2 * n_layers <= 65535
+  const int64_t row_bytes = (int64_t)n_kv_heads * head_dim * es;
+  if (row_bytes % 16 || (uintptr_t)cache % 16 || (uintptr_t)buf % 16 || (layer_stride * es) % 16 ||
+      (kv_stride * es) % 16)
+    return AAC_ERR_MISALIGNED;
+  if (row_bytes / 16 > 64 * kChunksPerLane * 1024) return AAC_ERR_UNSUPPORTED;
+  XferArgs a;
+  a.cache = (char*)const_cast<void*>(cache);
+  a.layer_stride = layer_stride * es;
+  a.kv_stride = kv_stride * es;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
+  a.block_table = block_table;
+  a.length = length;
+  a.row_chunks = (int32_t)(row_bytes / 16);
+  a.buf = (char*)buf;
+  dim3 grid((unsigned)cdiv(length, 4), (unsigned)(2 * n_layers));
+  if (export_)
+    hipLaunchKernelGGL(kv_xfer_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(kv_xfer_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AAC_OK : (int)e;
+}
+
+}  // namespace
+
+}  // namespace aac
+
+extern "C" int aac_kv_export_paged(const void* kv_cache, int64_t layer_stride, int64_t kv_stride,
+                                   int32_t n_layers, int64_t num_blocks, int32_t block_size,
+                                   int32_t n_kv_heads, int32_t head_dim,
+                                   const int32_t* block_table, int32_t max_blocks, int32_t length,
+                                   void* out, int32_t dtype, void* stream) {
+  return aac::xfer(true, kv_cache, layer_stride, kv_stride, n_layers, num_blocks, block_size,
+                   n_kv_heads, head_dim, block_table, max_blocks, length, out, dtype, stream);
+}
+
+extern "C" int aac_kv_import_paged(const void* src, void* kv_cache, int64_t layer_stride,
+                                   int64_t kv_stride, int32_t n_layers, int64_t num_blocks,
+                                   int32_t block_size, int32_t n_kv_heads, int32_t head_dim,
+                                   const int32_t* block_table, int32_t max_blocks, int32_t length,
+                                   int32_t dtype, void* stream) {
+  return aac::xfer(false, kv_cache, layer_stride, kv_stride, n_layers, num_blocks, block_size,
+                   n_kv_heads, head_dim, block_table, max_blocks, length, const_cast<void*>(src),
+                   dtype, stream);
+}

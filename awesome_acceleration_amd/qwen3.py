@@ -33,6 +33,7 @@ import torch.nn.functional as F
 
 from . import flash_attn_interface as fai
 from . import fused as fz
+from . import kv_transfer
 
 __all__ = ["Qwen3Config", "Qwen3ForCausalLM", "PagedKVCache", "StepMeta"]
 
@@ -113,6 +114,16 @@ class PagedKVCache:
     @property
     def nbytes(self) -> int:
         return self.storage.numel() * self.storage.element_size()
+
+    def export_request_kv(self, block_table, length: int, seqlen: int) -> dict:
+        """The reference's export_request_kv (model/model.py:386-390) for the
+        sequence whose blocks are ``block_table``."""
+        return kv_transfer.export_request_kv(self.storage, block_table, length, seqlen)
+
+    def import_request_kv(self, block_table, payload: dict, length: int) -> int:
+        """The reference's import_request_kv (model/model.py:392-401) into the
+        blocks ``block_table``; returns the payload's seqlen."""
+        return kv_transfer.import_request_kv(self.storage, block_table, payload, length)
 
 
 @dataclass

@@ -16,6 +16,9 @@ Also reported on the same line:
   decode_long   long-context GQA-4 decode (64 sequences, 32 query / 8 KV heads,
                 context ~ U[16384, 32768]): the split-K decode plus its
                 log-sum-exp reduction, HIP events, against 8 TB/s HBM;
+  kv_transfer   KV export (gather of one 2048-token request's 28 layers from the
+                paged cache into one contiguous buffer) and import, against
+                8 TB/s; the host-inclusive request export (PCIe) beside it;
   prefill       varlen causal prefill, 8 x 1024 tokens, 16/8 heads, bf16, with
                 the paged store in the same call, as TFLOP/s against the
                 2.5 PFLOP/s dense bf16 MFMA peak (roofline of that kernel);
@@ -68,11 +71,13 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-long", action="store_true", help="skip the long-context GQA-4 decode leg")
+    p.add_argument("--no-kv", action="store_true", help="skip the KV export/import leg")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine leg")
     p.add_argument("--e2e-seqs", type=int, default=256)
     p.add_argument("--e2e-in", type=int, default=1024)
     p.add_argument("--e2e-out", type=int, default=1024)
-    p.add_argument("--only", choices=["decode", "decode_long", "prefill", "e2e"], default=None,
+    p.add_argument("--only", choices=["decode", "decode_long", "kv_transfer", "prefill", "e2e"],
+                   default=None,
                    help="run one leg only (for profiling)")
     return p.parse_args()
 
@@ -192,6 +197,53 @@ def bench_decode_long(torch, fai, dev, args):
         "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "bytes_per_call": attend_bytes,
                      "traffic": None},
+    }
+
+
+# ----------------------------------------------------------------------------
+# KV export / import of one request: Qwen3-0.6B cache (28 layers, 8 KV heads),
+# 2048 tokens in 8 blocks of 256 drawn from a 2304-block pool
+# ----------------------------------------------------------------------------
+def bench_kv_transfer(torch, dev, args):
+    from awesome_acceleration_amd import kv_transfer as kt
+    L, nb, bs, hkv, d, length = 28, 2304, 256, 8, 128, 2048
+    st = torch.empty((L, 2, nb, bs, hkv, d), dtype=torch.bfloat16, device=dev)
+    st.view(torch.int16).random_(-30000, 30000, generator=torch.Generator(device=dev).manual_seed(args.seed))
+    bt = torch.randperm(nb, device=dev, generator=torch.Generator(device=dev).manual_seed(args.seed))
+    bt = bt[:length // bs].to(torch.int32)
+    buf = torch.empty((L, 2, length, hkv, d), dtype=torch.bfloat16, device=dev)
+    moved = 2 * buf.numel() * buf.element_size()  # read + write
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / args.steps / 1e3
+
+    t_ex = timed(lambda: kt.kv_export(st, bt, length, out=buf))
+    t_im = timed(lambda: kt.kv_import(buf, st, bt, length))
+    t0 = time.perf_counter()
+    for _ in range(3):
+        kt.export_request_kv(st, bt, length, length)
+    t_host = (time.perf_counter() - t0) / 3
+    del st
+    torch.cuda.empty_cache()
+    return {
+        "workload": "KV export / import of one 2048-token request, Qwen3-0.6B cache (28 layers, "
+                    "8 KV heads, head_dim 128, bf16), 8 blocks of 256 from a 2304-block pool",
+        "us_export": round(t_ex * 1e6, 2), "us_import": round(t_im * 1e6, 2),
+        "roofline": {"bound": "hbm", "achieved": round(moved / t_ex / 1e9, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(moved / t_ex / 1e9 / HBM_PEAK_GBS, 4),
+                     "bytes_per_call": moved, "traffic": None},
+        "import_GBs": round(moved / t_im / 1e9, 2),
+        "request_to_pinned_host_ms": round(t_host * 1e3, 3),
+        "request_to_pinned_host_GBs": round(moved / 2 / t_host / 1e9, 2),
     }
 
 
@@ -336,6 +388,8 @@ def main():
     if args.only in (None, "decode_long") and not args.no_long:
         res["decode_long"] = bench_decode_long(torch, fai, dev, args)
         torch.cuda.empty_cache()
+    if args.only in (None, "kv_transfer") and not args.no_kv:
+        res["kv_transfer"] = bench_kv_transfer(torch, dev, args)
     if args.only in (None, "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, fai, paged, dev, args)
     if args.only in (None, "e2e") and not args.no_e2e:
@@ -399,6 +453,8 @@ def main():
         }
     if "decode_long" in res:
         line["decode_long"] = res["decode_long"]
+    if "kv_transfer" in res:
+        line["kv_transfer"] = res["kv_transfer"]
     if "e2e" in res:
         line["e2e"] = res["e2e"]
     if not args.no_cpu:

@@ -243,6 +243,36 @@ int aac_qk_norm_rope_store(const void* qkv, int64_t qkv_tok_stride, int64_t n_to
 int aac_silu_mul(const void* gate_up, void* out, int64_t n_rows, int32_t intermediate,
                  int32_t dtype, void* stream);
 
+/*
+ * KV export: gather the first `length` tokens of one sequence from a paged
+ * cache into a contiguous buffer out[n_layers][2][length][Hkv][D] (index 0 =
+ * K, 1 = V).  Layer l's K cache starts at kv_cache + l * layer_stride and its
+ * V cache kv_stride elements after that (both [num_blocks, block_size, Hkv,
+ * D]); token t lives in block block_table[t / block_size] (table width
+ * max_blocks; length <= max_blocks * block_size).  Entries outside
+ * [0, num_blocks) export zeros.  Replaces the per-layer slices
+ * k_cache[slot, :length] / v_cache[slot, :length] of export_kv and
+ * export_request_kv (model/model.py:156-165, :386-390); the slot layout is
+ * block_table = [slot], block_size = max_seq_len.
+ */
+int aac_kv_export_paged(const void* kv_cache, int64_t layer_stride, int64_t kv_stride,
+                        int32_t n_layers, int64_t num_blocks, int32_t block_size,
+                        int32_t n_kv_heads, int32_t head_dim, const int32_t* block_table,
+                        int32_t max_blocks, int32_t length, void* out, int32_t dtype,
+                        void* stream);
+
+/*
+ * KV import: scatter src[n_layers][2][length][Hkv][D] into the paged cache
+ * through block_table (same layout and arguments as aac_kv_export_paged);
+ * entries outside [0, num_blocks) are skipped.  Replaces the per-layer
+ * copy_ of import_kv and import_request_kv (model/model.py:167-177, :392-401);
+ * cache_seqlens stays with the caller, as the reference sets it separately.
+ */
+int aac_kv_import_paged(const void* src, void* kv_cache, int64_t layer_stride, int64_t kv_stride,
+                        int32_t n_layers, int64_t num_blocks, int32_t block_size,
+                        int32_t n_kv_heads, int32_t head_dim, const int32_t* block_table,
+                        int32_t max_blocks, int32_t length, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -46,6 +46,13 @@ How each function is pinned (tests/test_oracle_pins.py):
 * ``paged_decode``: equals the last row of a causal prefill over the gathered
   context; invariant under permutation of physical block ids; context 1
   returns v0; against SDPA.
+* ``kv_export`` / ``kv_import``: in the slot layout (``block_size =
+  max_seq_len``, ``block_table = [slot]``) the export is exactly the
+  reference's ``k_cache[slot, :length]`` / ``v_cache[slot, :length]`` per
+  layer (model/model.py:156-165), the import exactly its
+  ``k_cache[slot, :length].copy_(k[:length])`` (:167-177), with every other
+  cache byte untouched; over a permuted pool, import-then-export returns the
+  payload and a block relabelling commutes with both.
 * bf16 helpers: bit-exact against ``torch.Tensor.to(torch.bfloat16)``
   (round-to-nearest-even) including ties, subnormals, inf and NaN.
 """
@@ -58,6 +65,8 @@ __all__ = [
     "bf16_bits_to_f32",
     "bf16_round",
     "kv_store",
+    "kv_export",
+    "kv_import",
     "prefill_metadata",
     "paged_slot_mapping",
     "decode_slot_mapping",
@@ -189,6 +198,36 @@ def gather_paged(cache: np.ndarray, block_table_row, n_tokens: int, block_size: 
     rows = cache.reshape((-1,) + tuple(cache.shape[2:]))
     p = np.arange(int(n_tokens), dtype=np.int64)
     return rows[bt[p // block_size] * block_size + p % block_size]
+
+
+def kv_export(storage: np.ndarray, block_table_row, length: int) -> np.ndarray:
+    """Export of one sequence (model/model.py:156-165, :386-390, paged form):
+    ``storage`` [L, 2, num_blocks, block_size, Hkv, D] -> [L, 2, length, Hkv, D]
+    with layer l, index c (0 = K, 1 = V) the first ``length`` token rows of
+    that cache.  Tokens whose block id is outside [0, num_blocks) read zeros."""
+    L, _, nb, bs = storage.shape[:4]
+    bt = np.asarray(block_table_row, dtype=np.int64)
+    p = np.arange(int(length), dtype=np.int64)
+    blk = bt[p // bs]
+    ok = (blk >= 0) & (blk < nb)
+    rows = storage.reshape((L, 2, nb * bs) + tuple(storage.shape[4:]))
+    out = np.zeros((L, 2, int(length)) + tuple(storage.shape[4:]), dtype=storage.dtype)
+    out[:, :, ok] = rows[:, :, (blk * bs + p % bs)[ok]]
+    return out
+
+
+def kv_import(src: np.ndarray, storage: np.ndarray, block_table_row, length: int) -> np.ndarray:
+    """Import (model/model.py:167-177, :392-401, paged form): writes src[:, :,
+    :length] into the sequence's token rows of ``storage`` in place (entries
+    outside [0, num_blocks) are skipped); returns ``storage``."""
+    L, _, nb, bs = storage.shape[:4]
+    bt = np.asarray(block_table_row, dtype=np.int64)
+    p = np.arange(int(length), dtype=np.int64)
+    blk = bt[p // bs]
+    ok = (blk >= 0) & (blk < nb)
+    rows = storage.reshape((L, 2, nb * bs) + tuple(storage.shape[4:]))
+    rows[:, :, (blk * bs + p % bs)[ok]] = src[:, :, :int(length)][:, :, ok]
+    return storage
 
 
 # ----------------------------------------------------------------------------

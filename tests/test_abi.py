@@ -53,6 +53,16 @@ def test_host_side_argument_rejection():
     # prefill: fp32 is not supported on the MFMA path
     assert L.aac_prefill_varlen(None, None, None, 0, 0, 0, None, None, 1, 1, 1, 16, 8, 128,
                                 1.0, 1, None, 0, 2, None) == -2
+    # KV export/import: unknown dtype, a table too short for the length, nothing to
+    # move, null pointers with work to do, a misaligned buffer
+    ex, im = L.aac_kv_export_paged, L.aac_kv_import_paged
+    assert ex(None, 0, 0, 2, 4, 16, 8, 128, None, 1, 8, None, 9, None) == -2
+    assert ex(None, 0, 0, 2, 4, 16, 8, 128, None, 2, 40, None, 0, None) == -5
+    assert im(None, None, 0, 0, 2, 4, 16, 8, 128, None, 2, 40, 0, None) == -5
+    assert ex(None, 0, 0, 0, 4, 16, 8, 128, None, 1, 8, None, 0, None) == 0
+    assert im(None, None, 0, 0, 2, 4, 16, 8, 128, None, 1, 0, 0, None) == 0
+    assert ex(None, 0, 0, 2, 4, 16, 8, 128, None, 1, 8, None, 0, None) == -1
+    assert ex(16, 0, 0, 2, 4, 16, 8, 128, 64, 1, 8, 24, 0, None) == -3
 
 
 def test_workspace_sizing():

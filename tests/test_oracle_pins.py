@@ -271,3 +271,59 @@ def test_decode_lse_splits_recombine():
     w1, w2 = np.exp(l1[0] - m), np.exp(l2 - m)
     comb = (w1[:, None] * o1[0] + w2[:, None] * o2[0]) / (w1 + w2)[:, None]
     assert np.allclose(comb, whole[0], atol=1e-12)
+
+
+def test_kv_export_import_reduce_to_reference_slot_slices():
+    # Slot layout (block_size = max_seq_len, block_table = [slot]): the export
+    # is the reference's k_cache[slot, :length] / v_cache[slot, :length] per
+    # layer (model/model.py:162-163) and the import its
+    # k_cache[slot, :length].copy_(k[:length]) (:174-175), evaluated with torch.
+    rs = np.random.RandomState(21)
+    L, S, lmax, hkv, d = 3, 4, 40, 2, 8
+    storage = rs.randint(0, 1 << 16, (L, 2, S, lmax, hkv, d)).astype(np.uint16)
+    slot, length = 2, 29
+    exp = oracle.kv_export(storage, [slot], length)
+    for layer in range(L):
+        for c in range(2):
+            ref = torch.from_numpy(storage[layer, c].view(np.int16))[slot, :length]
+            assert np.array_equal(exp[layer, c].view(np.int16), ref.numpy())
+    src = rs.randint(0, 1 << 16, (L, 2, length + 5, hkv, d)).astype(np.uint16)
+    got = oracle.kv_import(src, storage.copy(), [slot], length)
+    want = torch.from_numpy(storage.view(np.int16).copy())
+    for layer in range(L):
+        for c in range(2):
+            want[layer, c][slot, :length].copy_(torch.from_numpy(src[layer, c].view(np.int16))[:length])
+    assert np.array_equal(got.view(np.int16), want.numpy())
+
+
+def test_kv_export_import_round_trip_and_relabelling_over_a_permuted_pool():
+    rs = np.random.RandomState(22)
+    L, nb, bs, hkv, d, length = 2, 12, 4, 2, 4, 18
+    storage = rs.standard_normal((L, 2, nb, bs, hkv, d)).astype(np.float32)
+    bt = rs.permutation(nb)[:5].astype(np.int32)  # 5 blocks hold 18 tokens
+    exp = oracle.kv_export(storage, bt, length)
+    # rows of the export are the sequence's tokens in order
+    p = 13
+    assert np.array_equal(exp[1, 1, p], storage[1, 1, bt[p // bs], p % bs])
+    # import into a sentinel pool with another table, export again: the payload
+    sentinel = np.full_like(storage, 7.0)
+    bt2 = rs.permutation(nb)[:5].astype(np.int32)
+    back = oracle.kv_import(exp, sentinel.copy(), bt2, length)
+    assert np.array_equal(oracle.kv_export(back, bt2, length), exp)
+    touched = np.zeros((nb, bs), bool)
+    q = np.arange(length)
+    touched[bt2[q // bs], q % bs] = True
+    assert (back[:, :, ~touched] == 7.0).all()  # nothing else written
+    # relabelling the physical blocks commutes with the export
+    perm = rs.permutation(nb)
+    moved = np.empty_like(storage)
+    moved[:, :, perm] = storage
+    assert np.array_equal(oracle.kv_export(moved, perm[bt], length), exp)
+    # an invalid block id exports zeros and is skipped by the import
+    bad = bt.copy()
+    bad[2] = -1
+    e2 = oracle.kv_export(storage, bad, length)
+    assert not e2[:, :, 8:12].any() and np.array_equal(e2[:, :, :8], exp[:, :, :8])
+    s2 = sentinel.copy()
+    oracle.kv_import(exp, s2, bad, length)
+    assert (s2[:, :, bt[2]] == 7.0).all()  # the skipped block keeps its bytes
