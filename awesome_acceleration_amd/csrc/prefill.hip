@@ -343,22 +343,25 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     float m = -1e30f, l = 0.f;  // m: reference max of the raw scores (scale applied in exp2)
 
 
-    // Ring hazard: tile t+1 is written to stage (t+1)%3 after the barrier of
-    // iteration t-1, which every wave reaches only after it has finished all
-    // reads of tile t-2 (the last reader of that stage); the barrier of
-    // iteration t makes tile t+1 visible before the look-ahead scores read it.
+    // Ring schedule: iteration t writes tile t+1 (prefetched one tile
+    // earlier) into stage (t+1)%3, issues the loads of tile t+2, computes
+    // sub-tile 2t, then a barrier, then sub-tile 2t+1.  The stage's last
+    // reader, tile t-2, finished before the mid-tile barrier of iteration t-1,
+    // which every wave has passed; the mid-tile barrier of iteration t makes
+    // tile t+1 visible before the look-ahead of sub-tile 2t+1 reads it.  The
+    // LDS writes thus overlap sub-tile 2t instead of preceding a barrier.
     for (int t = 0; t < nt; ++t) {
       if (t + 1 < nt) stage_write(t + 1);
-      __syncthreads();
       if (t + 2 < nt) prefetch(t + 2);
-  #pragma unroll
+#pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
+        if (sub == 1) __syncthreads();
         const int j = 2 * t + sub;
         if (j < nsub) {  // wave-uniform
           // ---- causal mask (only sub-tiles that cross this wave's diagonal)
           const int kb = 32 * j;
           if (kb + 32 > w_full) {
-  #pragma unroll
+#pragma unroll
             for (int i = 0; i < 16; ++i) {
               const int key = kb + 8 * (i >> 2) + 4 * hl + (i & 3);
               sc[i] = key < my_lim ? sc[i] : -INFINITY;
@@ -366,7 +369,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
           }
           // ---- row max (the partner lane l^32 holds the other 16 keys)
           float mx = vmax3(sc[0], sc[1], sc[2]);
-  #pragma unroll
+#pragma unroll
           for (int i = 3; i < 15; i += 2) mx = vmax3(mx, sc[i], sc[i + 1]);
           mx = vmax(mx, sc[15]);
           {
@@ -385,9 +388,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
             const float alpha = fast_exp2((m - mn) * a.scale_log2);
             m = mn;
             l *= alpha;
-  #pragma unroll
+#pragma unroll
             for (int c = 0; c < 4; ++c)
-  #pragma unroll
+#pragma unroll
               for (int i = 0; i < 16; ++i) o[c][i] *= alpha;
           }
           // ---- look-ahead scores of sub-tile j+1 (MFMA) beside the
@@ -396,17 +399,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
           const float nb = -m * a.scale_log2;
           const f32x16 sn = scores(j + 1);
           float p[16];
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sc[i], a.scale_log2, nb));
           u32x4 pb[2];
-  #pragma unroll
+#pragma unroll
           for (int tt = 0; tt < 2; ++tt)
-  #pragma unroll
+#pragma unroll
             for (int w = 0; w < 4; ++w) pb[tt][w] = M::pack(p[8 * tt + 2 * w], p[8 * tt + 2 * w + 1]);
           // row sum of the rounded probabilities the PV product uses
-  #pragma unroll
+#pragma unroll
           for (int tt = 0; tt < 2; ++tt)
-  #pragma unroll
+#pragma unroll
             for (int w = 0; w < 4; ++w) l = M::dot2_ones(pb[tt][w], l);
           pv_step(j, pb);
           sc = sn;

@@ -70,6 +70,9 @@ def parse():
     p.add_argument("--partition", type=int, default=0, help="decode partition tokens (0=auto)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--prefill-seqs", type=int, default=8, help="prefill segments (default 8)")
+    p.add_argument("--prefill-len", type=int, default=1024, help="tokens per segment (default 1024)")
+    p.add_argument("--prefill-noncausal", action="store_true", help="prefill without the causal mask")
     p.add_argument("--no-long", action="store_true", help="skip the long-context GQA-4 decode leg")
     p.add_argument("--no-kv", action="store_true", help="skip the KV export/import leg")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine leg")
@@ -251,24 +254,27 @@ def bench_kv_transfer(torch, dev, args):
 # prefill: 8 x 1024 causal, 16/8 heads, store in the same call
 # ----------------------------------------------------------------------------
 def bench_prefill(torch, fai, paged, dev, args):
-    N, hq, hkv, d, bs, nseq, L = 8192, 16, 8, 128, 256, 8, 1024
+    hq, hkv, d, bs = 16, 8, 128, 256
+    nseq, L, causal = args.prefill_seqs, args.prefill_len, not args.prefill_noncausal
+    N = nseq * L
+    nb = -(-L // bs)  # blocks per sequence
     g = torch.Generator(device=dev).manual_seed(args.seed)
     qkv = torch.randn((N, (hq + 2 * hkv) * d), generator=g, device=dev).to(torch.bfloat16)
     q = qkv[:, :hq * d].view(N, hq, d)
     k = qkv[:, hq * d:(hq + hkv) * d].contiguous().view(N, hkv, d)  # post-RoPE copy
     v = qkv[:, (hq + hkv) * d:].view(N, hkv, d)                      # strided view
     rs = np.random.RandomState(args.seed)
-    perm = rs.permutation(32).astype(np.int32)
-    cu, _, sm = paged.build_prefill_metadata([L] * nseq, perm.reshape(nseq, 4), bs, dev)
-    kc = torch.zeros((32, bs, hkv, d), dtype=torch.bfloat16, device=dev)
+    perm = rs.permutation(nseq * nb).astype(np.int32)
+    cu, _, sm = paged.build_prefill_metadata([L] * nseq, perm.reshape(nseq, nb), bs, dev)
+    kc = torch.zeros((nseq * nb, bs, hkv, d), dtype=torch.bfloat16, device=dev)
     vc = torch.zeros_like(kc)
-    flops = 4 * hq * d * nseq * (L * (L + 1) // 2)
+    flops = 4 * hq * d * nseq * (L * (L + 1) // 2 if causal else L * L)
 
     def step():
-        return fai.varlen_prefill_with_kvcache(q, k, v, cu, L, kc, vc, sm, causal=True)
+        return fai.varlen_prefill_with_kvcache(q, k, v, cu, L, kc, vc, sm, causal=causal)
 
     def attend():
-        return fai.flash_attn_varlen_func(q, k, v, cu, cu, L, L, causal=True)
+        return fai.flash_attn_varlen_func(q, k, v, cu, cu, L, L, causal=causal)
 
     for _ in range(args.warmup):
         step()
@@ -443,7 +449,8 @@ def main():
     if "prefill" in res:
         pf = res["prefill"]
         line["prefill"] = {
-            "workload": "varlen causal prefill 8 x 1024 tokens, 16/8 heads, head_dim 128, bf16",
+            "workload": f"varlen {'non-causal' if args.prefill_noncausal else 'causal'} prefill "
+                        f"{args.prefill_seqs} x {args.prefill_len} tokens, 16/8 heads, head_dim 128, bf16",
             "us_attend": round(pf["t_attend"] * 1e6, 2),
             "us_step_with_store": round(pf["t_step"] * 1e6, 2),
             "roofline": {"bound": "mfma", "achieved": round(pf["tflops"], 2),
