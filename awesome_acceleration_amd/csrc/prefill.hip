@@ -137,7 +137,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   // resource, row stride and scalar offsets then live in SGPRs (a per-lane
   // resource would turn every buffer load into a readfirstlane loop).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wq = wave % WQ, wh = wave / WQ;
+  // Column slot (head wh, 32-query slot wq) of this wave.  Waves w and w+4 of
+  // a workgroup share a SIMD (measured), so wave w >= 4 takes slot 11 - w:
+  // on the causal diagonal each SIMD then pairs a wave with few visible keys
+  // with one that has many, instead of two heavy (or two light) waves.
+  const int cslot = wave < 4 ? wave : 11 - wave;
+  const int wq = cslot % WQ, wh = cslot / WQ;
   const int hl = lane >> 5;  // lane half
   const int col = lane & 31;
 
