@@ -75,6 +75,51 @@ def _ragged(lens_q, lens_k, hq, hkv, dtype, gpu, seed):
     return q, k, v, cq, ck
 
 
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_many_segments_persistent_schedule(gpu, hq, hkv, causal):
+    # 200 segments of 0..700 tokens: the persistent grid walks many zigzag
+    # rounds with holes in the last one and with q-block ranks that short
+    # segments lack (so both the early-loaded candidate and the fallback
+    # search pick items).  Every segment against torch SDPA in fp32 (GQA by
+    # repeat_interleave), a sample against the oracle.
+    print(f"case: many segments {hq}/{hkv} causal={causal}", flush=True)
+    rs = np.random.RandomState(7)
+    lens = rs.randint(0, 701, 200)
+    lens[:4] = [700, 0, 1, 129]
+    lens = lens.tolist()
+    q, k, v, cq, _ = _ragged(lens, lens, hq, hkv, torch.bfloat16, gpu, 9)
+    scale = 128 ** -0.5
+    out = fai.flash_attn_varlen_func(q, k, v, cq, cq, max(lens), max(lens), softmax_scale=scale,
+                                     causal=causal)
+    torch.cuda.synchronize()
+    g = hq // hkv
+    cu = cq.cpu().numpy()
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    worst = 0.0
+    for s in range(len(lens)):
+        a, b = int(cu[s]), int(cu[s + 1])
+        if a == b:
+            continue
+        qs = q[a:b].float().transpose(0, 1).contiguous()
+        ks = k[a:b].float().repeat_interleave(g, 1).transpose(0, 1).contiguous()
+        vs = v[a:b].float().repeat_interleave(g, 1).transpose(0, 1).contiguous()
+        ref = sdpa(qs, ks, vs, is_causal=causal, scale=scale).transpose(0, 1)
+        absv = sdpa(qs, ks, vs.abs(), is_causal=causal, scale=scale).transpose(0, 1)
+        err = (out[a:b].float() - ref).abs()
+        worst = max(worst, float(err.max()))
+        assert bool((err <= 2.0 ** -8 * (ref.abs() + absv) + 1e-3).all()), f"segment {s} (len {b - a})"
+    assert worst <= 2e-2, worst
+    for s in (0, 3, 17, 99, 150, 199):
+        a, b = int(cu[s]), int(cu[s + 1])
+        sub = np.array([0, b - a], np.int32)
+        ref = oracle.varlen_attention(f64(q[a:b]), f64(k[a:b]), f64(v[a:b]), sub, scale=scale,
+                                      causal=causal)
+        absv = oracle.varlen_attention(f64(q[a:b]), f64(k[a:b]), np.abs(f64(v[a:b])), sub,
+                                       scale=scale, causal=causal)
+        check_attention(out[a:b], ref, what=f"segment {s}", absv=absv)
+
+
 @pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("causal", [True, False])
