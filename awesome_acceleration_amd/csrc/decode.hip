@@ -13,17 +13,24 @@
 //   lane li holds head dims [8*li, 8*li+8) and loads them with one 16-byte
 //   global load (two for fp32), so a wavefront reads 4 token rows (4 x 256 B
 //   in bf16) per load instruction and U=8 rows per DPP row (4 for G=8) are in
-//   flight before the first use.  The 16 rows of a workgroup walk the
-//   partition in lock step (row slot r takes tokens t0 + r, t0 + r + 16, ...).
-//   K/V are read with non-temporal loads: each byte is used once per step, so
-//   it should not displace anything from L2/MALL (measured +10% bandwidth).
-//   Power-of-two block sizes use shift/mask for the block-table lookup.
+//   flight before the first use: the block-table entries of an iteration are
+//   loaded one iteration ahead and all K/V loads are issued before any math
+//   (with in-order load counters, a block-table load waited for in between
+//   would also wait for every earlier K/V load).  The 16 rows of a workgroup
+//   walk the partition in lock step (row slot r takes tokens t0 + r,
+//   t0 + r + 16, ...); slots past the partition end re-read token t0's row
+//   (finite, probability 0) so the loads never branch.  K/V are read with
+//   non-temporal loads: each byte is used once per step, so it should not
+//   displace anything from L2/MALL (measured +10% bandwidth).  Power-of-two
+//   block sizes use shift/mask for the block-table lookup.
 //
 // Softmax
 //   Each DPP row keeps its own online-softmax state (running max m, running
 //   sum l, fp32 accumulator for its 8 dims x G heads; Milakov & Gimelshein
-//   2018), in the log2 domain (scores are pre-multiplied by scale*log2 e and
-//   exponentiated with v_exp_f32).  The 16 row states of a workgroup are
+//   2018), in the log2 domain (exponentiated with v_exp_f32).  bf16/fp16: q.k
+//   is v_dot2 on the packed rows, the probabilities are rounded to the input
+//   type and P.V is v_dot2 over V words paired across two tokens (v_perm);
+//   fp32: unpacked fp32 FMAs with q pre-scaled.  The 16 row states of a workgroup are
 //   merged at the end (cross-row shuffles inside a wave, LDS across waves).
 //   A sequence whose context spans one partition writes the final output
 //   directly; longer contexts write a normalised partial output and its
