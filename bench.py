@@ -16,6 +16,9 @@ Also reported on the same line:
   decode_long   long-context GQA-4 decode (64 sequences, 32 query / 8 KV heads,
                 context ~ U[16384, 32768]): the split-K decode plus its
                 log-sum-exp reduction, HIP events, against 8 TB/s HBM;
+  tp2_rank      the decode and prefill kernels at one rank's share of TP=2
+                (8 query / 4 KV heads), the shape one GPU runs when the heads
+                are split across two (no collective is run or timed);
   kv_transfer   KV export (gather of one 2048-token request's 28 layers from the
                 paged cache into one contiguous buffer) and import, against
                 8 TB/s; the host-inclusive request export (PCIe) beside it;
@@ -75,11 +78,13 @@ def parse():
     p.add_argument("--prefill-noncausal", action="store_true", help="prefill without the causal mask")
     p.add_argument("--no-long", action="store_true", help="skip the long-context GQA-4 decode leg")
     p.add_argument("--no-kv", action="store_true", help="skip the KV export/import leg")
+    p.add_argument("--no-tp2", action="store_true", help="skip the TP=2 per-rank shape leg")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine leg")
     p.add_argument("--e2e-seqs", type=int, default=256)
     p.add_argument("--e2e-in", type=int, default=1024)
     p.add_argument("--e2e-out", type=int, default=1024)
-    p.add_argument("--only", choices=["decode", "decode_long", "kv_transfer", "prefill", "e2e"],
+    p.add_argument("--only", choices=["decode", "decode_long", "tp2_rank", "kv_transfer", "prefill",
+                                      "e2e"],
                    default=None,
                    help="run one leg only (for profiling)")
     return p.parse_args()
@@ -121,8 +126,8 @@ def decode_bytes(x):
     return kv + qo, kv + qo + store
 
 
-def bench_decode(torch, fai, dev, args):
-    x = make_decode_inputs(torch, dev, args.seed)
+def bench_decode(torch, fai, dev, args, hq=16, hkv=8):
+    x = make_decode_inputs(torch, dev, args.seed, hq=hq, hkv=hkv)
     attend_bytes, step_bytes = decode_bytes(x)
     maxctx = int(x["ctx"].max())
 
@@ -253,8 +258,8 @@ def bench_kv_transfer(torch, dev, args):
 # ----------------------------------------------------------------------------
 # prefill: 8 x 1024 causal, 16/8 heads, store in the same call
 # ----------------------------------------------------------------------------
-def bench_prefill(torch, fai, paged, dev, args):
-    hq, hkv, d, bs = 16, 8, 128, 256
+def bench_prefill(torch, fai, paged, dev, args, hq=16, hkv=8):
+    d, bs = 128, 256
     nseq, L, causal = args.prefill_seqs, args.prefill_len, not args.prefill_noncausal
     N = nseq * L
     nb = -(-L // bs)  # blocks per sequence
@@ -394,6 +399,23 @@ def main():
     if args.only in (None, "decode_long") and not args.no_long:
         res["decode_long"] = bench_decode_long(torch, fai, dev, args)
         torch.cuda.empty_cache()
+    if args.only in (None, "tp2_rank") and not args.no_tp2:
+        dec2 = bench_decode(torch, fai, dev, args, hq=8, hkv=4)
+        pf2 = bench_prefill(torch, fai, paged, dev, args, hq=8, hkv=4)
+        res["tp2_rank"] = {
+            "workload": "one tensor-parallel rank of TP=2 (8 q / 4 kv heads): the 256-sequence decode "
+                        "attention (context U[1024,2047], shuffled pool) and the 8 x 1024 causal prefill",
+            "decode": {"us_per_launch": round(dec2["t_attend"] * 1e6, 2),
+                       "achieved": round(dec2["achieved"], 2), "unit": "GB/s",
+                       "frac": round(dec2["achieved"] / HBM_PEAK_GBS, 4),
+                       "bytes_per_launch": dec2["attend_bytes"]},
+            "prefill": {"us_attend": round(pf2["t_attend"] * 1e6, 2),
+                        "achieved": round(pf2["tflops"], 2), "unit": "TFLOP/s",
+                        "frac": round(pf2["tflops"] / BF16_PEAK_TFLOPS, 4),
+                        "flops_per_launch": pf2["flops"]},
+        }
+        del dec2
+        torch.cuda.empty_cache()
     if args.only in (None, "kv_transfer") and not args.no_kv:
         res["kv_transfer"] = bench_kv_transfer(torch, dev, args)
     if args.only in (None, "prefill") and not args.no_prefill:
@@ -460,6 +482,8 @@ def main():
         }
     if "decode_long" in res:
         line["decode_long"] = res["decode_long"]
+    if "tp2_rank" in res:
+        line["tp2_rank"] = res["tp2_rank"]
     if "kv_transfer" in res:
         line["kv_transfer"] = res["kv_transfer"]
     if "e2e" in res:
