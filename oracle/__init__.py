@@ -1,6 +1,6 @@
 """CPU oracle for the attention hot path (test infrastructure only).
 
-This package is the CHECKER, not the product.  Only ``tests/``,
+This package is the test oracle, not the product.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it; the library under ``awesome_acceleration_amd`` never does, and its
 HIP entry points fail loudly when the compiled extension is missing.
