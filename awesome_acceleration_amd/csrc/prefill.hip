@@ -64,6 +64,7 @@ struct Args {
   float scale_log2;
   u16* out;
   int32_t n_qblocks;  // q-blocks of the longest segment
+  int32_t max_k;      // max_seqlen_k: bounds every segment's key count
 };
 
 template <bool F16> struct Mfma;
@@ -193,7 +194,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     it.q_beg = q0;
     it.Lq = q1 - q0;
     it.k_beg = k0;
-    it.Lk = k1 - k0;
+    // clamped to max_seqlen_k, which the host checked against the 32-bit
+    // staging offsets (a caller that understates it gets truncated
+    // attention, never an out-of-range read)
+    it.Lk = min(k1 - k0, a.max_k);
     const int nqb = (it.Lq + BQ - 1) / BQ;
     it.qb = CAUSAL ? nqb - 1 - z : z;
     return z < nqb;
@@ -531,11 +535,10 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
                           int32_t head_dim, float scale, int32_t causal, void* out,
                           int64_t out_tok_stride, int32_t dtype, hipStream_t stream,
                           bool launch) {
-  (void)max_seqlen_k;
   if (dtype != AAC_DTYPE_BF16 && dtype != AAC_DTYPE_FP16) return AAC_ERR_UNSUPPORTED;
   if (head_dim != pf::D) return AAC_ERR_UNSUPPORTED;
-  if (n_seqs < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_seqlen_q < 0 || q_tok_stride < 0 ||
-      k_tok_stride < 0 || v_tok_stride < 0 || out_tok_stride < 0)
+  if (n_seqs < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_seqlen_q < 0 || max_seqlen_k < 0 ||
+      q_tok_stride < 0 || k_tok_stride < 0 || v_tok_stride < 0 || out_tok_stride < 0)
     return AAC_ERR_INVALID_ARGUMENT;
   if (n_q_heads % n_kv_heads) return AAC_ERR_SHAPE;
   const int g = n_q_heads / n_kv_heads;
@@ -570,6 +573,7 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
   a.hkv = n_kv_heads;
   a.scale_log2 = scale * kLog2e;
   a.out = (u16*)out;
+  a.max_k = max_seqlen_k;
   const bool f16 = dtype == AAC_DTYPE_FP16;
   int n_cu = 0;
   int rc = pf::device_cu_count(&n_cu);

@@ -181,6 +181,10 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     qs, ks, vs = _prefill_checks(q, k, v, cu_seqlens_q, cu_seqlens_k)
     scale = q.shape[-1] ** -0.5 if softmax_scale is None else float(softmax_scale)
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if q.shape[0] == 0:
+        return out
+    if k.shape[0] == 0:  # no key anywhere: every row sees none
+        return out.zero_()
     rc = _lib.lib().aac_prefill_varlen(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), qs, ks, vs, cu_seqlens_q.data_ptr(),
         cu_seqlens_k.data_ptr(), cu_seqlens_q.shape[0] - 1, int(max_seqlen_q), int(max_seqlen_k),
@@ -232,8 +236,8 @@ def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
     qf = q.reshape(B * Tq, Hq, D)
     kf = k.reshape(B * Tk, k.shape[2], D)
     vf = v.reshape(B * Tk, v.shape[2], D)
-    cu_q = torch.arange(0, (B + 1) * Tq, Tq, dtype=torch.int32, device=q.device)
-    cu_k = torch.arange(0, (B + 1) * Tk, Tk, dtype=torch.int32, device=q.device)
+    steps = torch.arange(B + 1, dtype=torch.int32, device=q.device)
+    cu_q, cu_k = steps * Tq, steps * Tk  # (valid for empty sequences too)
     out = flash_attn_varlen_func(qf, kf, vf, cu_q, cu_k, Tq, Tk, softmax_scale=softmax_scale,
                                  causal=causal)
     return out.view(B, Tq, Hq, D)

@@ -187,3 +187,29 @@ def test_decode_equals_last_prefill_row(gpu):
     torch.cuda.synchronize()
     diff = (dec.float() - pre[rows].float()).abs().max().item()
     assert diff <= 2 ** -7, diff
+
+
+def test_empty_sequences_and_understated_max_seqlen_k(gpu):
+    print("case: empty sequences, understated max_seqlen_k", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q = torch.randn((2, 7, 16, 128), generator=g, device=gpu).to(torch.bfloat16)
+    none = torch.empty((2, 0, 8, 128), dtype=torch.bfloat16, device=gpu)
+    out = fai.flash_attn_func(q, none, none)  # no keys: every row is zero
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and not out.any()
+    assert fai.flash_attn_func(q[:, :0], none, none).shape == (2, 0, 16, 128)
+    # A max_seqlen_k below the real key count is a caller error (as in FA2); the
+    # kernel clamps every segment to it, so the result is attention over the
+    # first max_seqlen_k keys and no read leaves the segment.
+    lens_q, lens_k = [40, 9], [300, 120]
+    qv, k, v, cq, ck = _ragged(lens_q, lens_k, 16, 8, torch.bfloat16, gpu, 6)
+    out = fai.flash_attn_varlen_func(qv, k, v, cq, ck, 40, 100, causal=False)
+    torch.cuda.synchronize()
+    kk, vv = f64(k), f64(v)
+    ckn = ck.cpu().numpy()
+    keep = np.concatenate([np.arange(ckn[s], ckn[s] + 100) for s in range(2)])
+    ck_t = np.array([0, 100, 200], np.int32)
+    ref = oracle.varlen_attention(f64(qv), kk[keep], vv[keep], cq.cpu().numpy(), ck_t, causal=False)
+    absv = oracle.varlen_attention(f64(qv), kk[keep], np.abs(vv[keep]), cq.cpu().numpy(), ck_t,
+                                   causal=False)
+    check_attention(out, ref, what="clamped keys", absv=absv)
