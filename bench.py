@@ -11,8 +11,10 @@ q read, output written, new K/V read and stored) divided by the step time,
 inputs resident in HBM.
 
 Also reported on the same line:
-  roofline      the decode attention launch alone (aac_decode_paged), timed
-                with HIP events on the launch stream, against 8 TB/s HBM;
+  roofline      the decode attention launch alone (aac_decode_paged): HIP
+                events on the launch stream around back-to-back launches,
+                divided by their count (every per-launch figure below is
+                timed the same way), against 8 TB/s HBM;
   decode_long   long-context GQA-4 decode (64 sequences, 32 query / 8 KV heads,
                 context ~ U[16384, 32768]): the split-K decode plus its
                 log-sum-exp reduction, HIP events, against 8 TB/s HBM;
@@ -126,6 +128,20 @@ def decode_bytes(x):
     return kv + qo, kv + qo + store
 
 
+def launch_avg(torch, fn, n):
+    """Average duration of one launch of ``fn`` (seconds): HIP events on the
+    current stream around ``n`` back-to-back launches, so the per-launch host
+    dispatch latency overlaps the previous launch as in a running engine."""
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(n):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n / 1e3
+
+
 def bench_decode(torch, fai, dev, args, hq=16, hkv=8):
     x = make_decode_inputs(torch, dev, args.seed, hq=hq, hkv=hkv)
     attend_bytes, step_bytes = decode_bytes(x)
@@ -155,15 +171,7 @@ def bench_decode(torch, fai, dev, args, hq=16, hkv=8):
     torch.cuda.synchronize()
     t_step = (time.perf_counter() - t0) / args.steps
     # the attention launch alone, HIP events on the launch stream
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    for a, b in evs:
-        a.record()
-        attend()
-        b.record()
-    torch.cuda.synchronize()
-    t_att = sum(a.elapsed_time(b) for a, b in evs) / len(evs) / 1e3
+    t_att = launch_avg(torch, attend, args.steps)
     achieved = attend_bytes / t_att / 1e9
     return dict(
         t_step=t_step, step_bytes=step_bytes, attend_bytes=attend_bytes, t_attend=t_att,
@@ -187,15 +195,7 @@ def bench_decode_long(torch, fai, dev, args):
 
     for _ in range(args.warmup):
         attend()
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    for a, b in evs:
-        a.record()
-        attend()
-        b.record()
-    torch.cuda.synchronize()
-    t = sum(a.elapsed_time(b) for a, b in evs) / len(evs) / 1e3
+    t = launch_avg(torch, attend, args.steps)
     ach = attend_bytes / t / 1e9
     return {
         "workload": "paged decode attend, 64 seqs, 32 q / 8 kv heads (GQA-4), head_dim 128, "
@@ -225,14 +225,7 @@ def bench_kv_transfer(torch, dev, args):
     def timed(fn):
         for _ in range(args.warmup):
             fn()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(args.steps):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / args.steps / 1e3
+        return launch_avg(torch, fn, args.steps)
 
     t_ex = timed(lambda: kt.kv_export(st, bt, length, out=buf))
     t_im = timed(lambda: kt.kv_import(buf, st, bt, length))
@@ -290,14 +283,7 @@ def bench_prefill(torch, fai, paged, dev, args, hq=16, hkv=8):
         step()
     torch.cuda.synchronize()
     t_step = (time.perf_counter() - t0) / args.steps
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    for a, b in evs:
-        a.record()
-        attend()
-        b.record()
-    torch.cuda.synchronize()
-    t_att = sum(a.elapsed_time(b) for a, b in evs) / len(evs) / 1e3
+    t_att = launch_avg(torch, attend, args.steps)
     return dict(t_step=t_step, t_attend=t_att, flops=flops, tflops=flops / t_att / 1e12)
 
 
