@@ -9,6 +9,12 @@
 //   A workgroup owns one KV head of one sequence over a partition of
 //   `part_tokens` consecutive context tokens and serves all G = Hq/Hkv query
 //   heads that share that KV head, so each K/V byte is read from HBM once.
+//   Without a split (up to 1024 sequences), blockIdx.z is a rank in
+//   descending context-length order, which every workgroup maps to its
+//   sequence: the dispatcher, which hands out workgroups in index order as
+//   slots free up, then starts long sequences first and fills the end of the
+//   launch with short ones instead of leaving a few long ones running alone
+//   (256 sequences of 1024..2047 tokens: 264 -> 254 us).
 //   Inside the workgroup every 16-lane DPP row owns one token row at a time:
 //   lane li holds head dims [8*li, 8*li+8) and loads them with one 16-byte
 //   global load (two for fp32), so a wavefront reads 4 token rows (4 x 256 B
@@ -41,6 +47,9 @@
 // each KV head is read exactly once, 2 * Hkv * D * elem_bytes per token, plus
 // q and out; the reduction adds 2 * B * Hq * P * (D + 1) * 4 bytes when split.
 
+#include <algorithm>
+#include <climits>
+
 #include "aac_common.h"
 
 namespace aac {
@@ -70,6 +79,8 @@ struct DecodeArgs {
   int32_t n_parts;
   int32_t part_tokens;
   int32_t bs_shift;  // log2(block_size) when it is a power of two
+  int32_t lpt;       // 1: blockIdx.z is a rank in descending context order
+  int32_t lpt_max;   // context bound the length classes are scaled to
 };
 
 // Raw storage for the 8 elements one lane owns in one token row.
@@ -110,6 +121,74 @@ __device__ __forceinline__ int parts_of(const DecodeArgs& a, int ctx) {
   return n > a.n_parts ? a.n_parts : n;
 }
 
+// Sequence of rank `rank` in descending context-length order, by length
+// class: class c = ctx * 64 / (lpt_max + 1) (64 classes, longest first),
+// index order inside a class.  Counts, prefix sums and ballots do not depend
+// on timing, so every workgroup derives the same bijection rank -> sequence:
+//   1. histogram of the classes (LDS atomics; the counts are exact),
+//   2. one wavefront scans the 64 counts and finds the class and position of
+//      `rank`,
+//   3. per 64-sequence chunk a ballot of "in that class" and its popcounts
+//      give each sequence its position inside the class.
+constexpr int kLptMaxSeqs = 1024;
+constexpr int kLptClasses = 64;
+__device__ __forceinline__ int seq_of_rank(const DecodeArgs& a, int rank, int tid) {
+  __shared__ int s_cnt[kLptClasses];
+  __shared__ int s_wcnt[kLptMaxSeqs / 64];
+  __shared__ int s_sel[2];
+  __shared__ int s_pick;
+  const int n = a.n_seqs, lane = tid & 63, wave = tid >> 6;
+  if (tid < kLptClasses) s_cnt[tid] = 0;
+  __syncthreads();
+  int cls[kLptMaxSeqs / 256];  // descending class index of sequences tid + 256k (-1: none)
+#pragma unroll
+  for (int k = 0; k < kLptMaxSeqs / 256; ++k) {
+    const int i = tid + 256 * k;
+    cls[k] = -1;
+    if (i < n) {
+      const int64_t c = (int64_t)context_len(a, i) * kLptClasses / ((int64_t)a.lpt_max + 1);
+      cls[k] = kLptClasses - 1 - (int)(c < kLptClasses - 1 ? c : kLptClasses - 1);
+      atomicAdd(&s_cnt[cls[k]], 1);
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int v = s_cnt[lane];
+    int incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off);
+      if (lane >= off) incl += t;
+    }
+    if (rank >= incl - v && rank < incl) {
+      s_sel[0] = lane;
+      s_sel[1] = rank - (incl - v);
+    }
+  }
+  __syncthreads();
+  const int csel = s_sel[0], psel = s_sel[1];
+  unsigned long long bal[kLptMaxSeqs / 256];
+#pragma unroll
+  for (int k = 0; k < kLptMaxSeqs / 256; ++k) {
+    bal[k] = __ballot(cls[k] == csel);
+    if (lane == 0) s_wcnt[4 * k + wave] = __popcll(bal[k]);
+  }
+  __syncthreads();
+  int base = 0;
+#pragma unroll
+  for (int k = 0; k < kLptMaxSeqs / 256; ++k) {
+    const int chunk = 4 * k + wave;  // 64-sequence chunks in index order
+    int before = base;
+    for (int m = 4 * k; m < chunk; ++m) before += s_wcnt[m];
+    const int pos = before + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal[k] >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((unsigned)bal[k], 0u));
+    if (cls[k] == csel && pos == psel) s_pick = tid + 256 * k;
+    for (int m = 4 * k; m < 4 * k + 4; ++m) base += s_wcnt[m];
+  }
+  __syncthreads();
+  return s_pick;
+}
+
 template <Dt DT>
 __device__ __forceinline__ void store_out2(void* out, int64_t idx, float x0, float x1) {
   if constexpr (DT == Dt::FP32) {
@@ -120,14 +199,20 @@ __device__ __forceinline__ void store_out2(void* out, int64_t idx, float x0, flo
 }
 
 template <Dt DT, int G, int U, bool POW2>
-__global__ __launch_bounds__(256) void decode_paged_kernel(DecodeArgs a) {
+// Occupancy: with G <= 2 the kernel fits 128 VGPRs, i.e. four workgroups per
+// CU (16 wavefronts); larger groups hold more accumulators.
+__global__ __launch_bounds__(256, G <= 2 ? 4 : 2) void decode_paged_kernel(DecodeArgs a) {
   constexpr int ES = Elem<DT>::kBytes;
   const int h = blockIdx.x;  // the KV heads of one token range are dispatched together
   const int part = blockIdx.y;
-  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  // Longest contexts first: the dispatcher hands out workgroups in index
+  // order as slots free up, so the short sequences fill the tail instead of
+  // a few long ones running alone at the end.
+  const int b = a.lpt ? __builtin_amdgcn_readfirstlane(seq_of_rank(a, blockIdx.z, tid))
+                     : (int)blockIdx.z;  // wave-uniform (SGPR) either way
   const int ctx = context_len(a, b);
   const int np = parts_of(a, ctx);
-  const int tid = threadIdx.x;
 
   if (part >= np) {
     if (part == 0) {  // empty context: zeros (FA2 convention)
@@ -523,6 +608,12 @@ static int decode_common(const void* q, int64_t q_seq_stride, const void* k_cach
   a.n_parts = plan.n_parts;
   a.part_tokens = plan.part_tokens;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  // length order only without a split: split partitions are already
+  // uniform work units, and the ordering costs every workgroup a few barriers
+  a.lpt = plan.n_parts == 1 && n_seqs >= 2 && n_seqs <= kLptMaxSeqs;
+  a.lpt_max = max_context_len > 0
+                  ? max_context_len
+                  : (int32_t)std::min<int64_t>((int64_t)max_blocks_per_seq * block_size, INT32_MAX);
   if (plan.ws_bytes) {
     a.ws_o = reinterpret_cast<float*>(workspace);
     a.ws_lse = a.ws_o + (size_t)n_seqs * n_q_heads * plan.n_parts * kHeadDim;

@@ -246,3 +246,26 @@ def test_decode_edge_cases_and_block_relabelling(gpu):
                             partition_tokens=128)
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("B", [700, 1024, 1025])
+def test_decode_many_sequences_dispatch_order(gpu, B):
+    # Up to 1024 sequences the kernel dispatches them longest-first through a
+    # rank -> sequence mapping every workgroup derives on its own; a mapping
+    # that is not a bijection would leave some sequence's output unwritten.
+    # 1025 sequences take the identity order.
+    print(f"case: decode dispatch order B={B}", flush=True)
+    rs = np.random.RandomState(B)
+    hq, hkv, bs = 8, 2, 16
+    ctx = rs.randint(1, 200, B).astype(np.int32)
+    ctx[rs.randint(B, size=20)] = 200  # ties in the longest class
+    q, kc, vc, _, _, bt = _random_paged(B, hq, hkv, ctx, bs, B, gpu)
+    out = torch.full((B, hq, 128), float("nan"), device=gpu, dtype=torch.bfloat16)
+    fai.decode_paged(q, kc, vc, torch.from_numpy(bt).to(gpu), torch.from_numpy(ctx).to(gpu), 0.1,
+                     max_context_len=200, out=out)
+    torch.cuda.synchronize()
+    kc_np, vc_np, q_np = f64(kc), f64(vc), f64(q)
+    ref = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), 0.1)
+    absv = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), 0.1, abs_v=True)
+    check_attention(out, np.stack([ref[b] for b in range(B)]), what=f"B={B}",
+                    absv=np.stack([absv[b] for b in range(B)]))
