@@ -30,6 +30,11 @@
 //     segment, q-block) are taken heaviest causal q-blocks first in a zigzag
 //     that pairs heavy with light items, and each workgroup issues the next
 //     item's Q and first K/V tile before the current item's epilogue.
+//   * Store in the same kernel (llm.py:171-174, the causal self-attention
+//     call): each item writes its own q-block's K/V rows into the cache
+//     through slot_mapping after its output, while the next item's loads are
+//     in flight -- one launch instead of a store kernel and an attention
+//     kernel (8 x 1024 Qwen3-0.6B layer: 60.9 -> 53.1 us).
 //
 // FLOPs per launch (the MFMA roofline): 4 * Hq * D * sum over segments of the
 // visible (query, key) pairs, i.e. 4*Hq*D*L(L+1)/2 per causal segment.
@@ -65,6 +70,13 @@ struct Args {
   u16* out;
   int32_t n_qblocks;  // q-blocks of the longest segment
   int32_t max_k;      // max_seqlen_k: bounds every segment's key count
+  // KV-cache store in the same kernel (self-attention, cu_q == cu_k): token
+  // t's K/V rows go to cache row slots[t] of the [num_rows, hkv, D] caches
+  u16* kc;
+  u16* vc;
+  const int64_t* slots;
+  int64_t num_rows;
+  int32_t n_tok;  // k/v tokens the store covers
 };
 
 template <bool F16> struct Mfma;
@@ -118,7 +130,7 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-template <int G, bool CAUSAL, bool F16>
+template <int G, bool CAUSAL, bool F16, bool STORE>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   constexpr int WH = G;                // head slots per workgroup (one head per wave)
   constexpr int WQ = kWaves / WH;      // 32-query slots per workgroup
@@ -236,9 +248,96 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     for (int t = 0; t < 8; ++t) qf[t] = *reinterpret_cast<const u32x4*>(qp + 16 * t);
   };
 
+  // ---- the KV-cache store (STORE).  Each item stores the K/V rows of its own
+  // q-block (its queries' rows taken as keys, since cu_q == cu_k) for its KV
+  // head: loaded right after its tile loop (they were staged moments before,
+  // so they come from L2), ahead of the next item's loads so that waiting
+  // for them never waits for those, and written after the output.  The item
+  // of rank 0 of a segment also stores the q-blocks no item owns (a
+  // max_seqlen_q below the segment's length), and workgroup 0 the tokens
+  // before cu[0] and from cu[n] on.  Every token's rows are thus written at
+  // least once; a row written twice gets the same bytes both times.  The
+  // store's arguments are read from the kernel-argument segment where they
+  // are used (the empty asm hides the pointer's origin), so they hold no
+  // SGPRs through the tile loop.
+  typedef const Args __attribute__((address_space(4))) KArgs;
+  auto sargs = [&]() {
+    KArgs* p = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return p;
+  };
+  auto copy_span = [&](int64_t t0, int64_t t1, int h0, int h1) {  // the rare paths
+    KArgs* sa = sargs();
+    t0 = max(t0, (int64_t)0);
+    t1 = min(t1, (int64_t)sa->n_tok);
+    const int nh = h1 - h0;
+    const int64_t n = t1 > t0 ? (t1 - t0) * nh : 0;
+    for (int64_t r = tid >> 4; r < n; r += kThreads / 16) {
+      const int64_t tok = t0 + r / nh;
+      const int hh = h0 + (int)(r % nh);
+      const int64_t sl = sa->slots[tok];
+      const u32x4 kx = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + hh * D + (tid & 15) * 8);
+      const u32x4 vx = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + hh * D + (tid & 15) * 8);
+      if ((uint64_t)sl < (uint64_t)sa->num_rows) {
+        const int64_t dst = (sl * a.hkv + hh) * D + (tid & 15) * 8;
+        *reinterpret_cast<u32x4*>(sa->kc + dst) = kx;
+        *reinterpret_cast<u32x4*>(sa->vc + dst) = vx;
+      }
+    }
+  };
+  // own rows of an item: thread rows (tid >> 4) + 32 i, 16 B at dim 8 (tid & 15);
+  // rows past the q-block repeat its last row (same bytes to the same slot)
+  constexpr int NI = BQ / 32 < 4 ? BQ / 32 : 4;  // passes issued early (G = 1 has 8)
+  int64_t csl[NI];
+  u32x4 ck[NI], cv[NI];
+  auto own_load = [&](KArgs* sa, const Item& it, int pass, int64_t& sl, u32x4& kx, u32x4& vx) {
+    const int r0 = it.qb * BQ;
+    const int nr = min(BQ, it.Lq - r0);  // >= 1 for an existing item
+    const int rr = min((tid >> 4) + 32 * pass, nr - 1);
+    const int64_t t = (int64_t)it.k_beg + r0 + rr;
+    const int64_t tok = min(t, (int64_t)sa->n_tok - 1);
+    sl = t < sa->n_tok ? sa->slots[tok] : -1;
+    kx = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + it.h * D + (tid & 15) * 8);
+    vx = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + it.h * D + (tid & 15) * 8);
+  };
+  auto own_store = [&](KArgs* sa, const Item& it, int64_t sl, const u32x4& kx, const u32x4& vx) {
+    if ((uint64_t)sl < (uint64_t)sa->num_rows) {
+      const int64_t dst = (sl * a.hkv + it.h) * D + (tid & 15) * 8;
+      *reinterpret_cast<u32x4*>(sa->kc + dst) = kx;
+      *reinterpret_cast<u32x4*>(sa->vc + dst) = vx;
+    }
+  };
+  auto store_rest = [&](const Item& it) {  // after the early passes' stores
+    KArgs* sa = sargs();
+#pragma unroll
+    for (int i = NI; i < BQ / 32; ++i) {
+      int64_t sl;
+      u32x4 kx, vx;
+      own_load(sa, it, i, sl, kx, vx);
+      own_store(sa, it, sl, kx, vx);
+    }
+    const int nqb = (it.Lq + BQ - 1) / BQ;
+    if (nqb - 1 - it.qb == 0 && nqb > a.n_qblocks) {  // rank 0 (causal numbering)
+      const int lo = nqb - a.n_qblocks;               // q-blocks [lo, nqb) have items
+      copy_span(it.k_beg, it.k_beg + (int64_t)lo * BQ, it.h, it.h + 1);
+    }
+  };
+  // workgroup 0: tokens outside [cu[0], cu[n]) (lanes 0 / 1 load the bounds now)
+  const int edge_cu = STORE && blockIdx.x == 0 ? a.cu_q[(lane & 1) ? a.n_seqs : 0] : 0;
+  auto store_edges = [&]() {
+    if (STORE && blockIdx.x == 0) {
+      const int c0 = __builtin_amdgcn_readlane(edge_cu, 0), cn = __builtin_amdgcn_readlane(edge_cu, 1);
+      copy_span(0, c0, 0, a.hkv);
+      copy_span(cn, sargs()->n_tok, 0, a.hkv);
+    }
+  };
+
   int k = 0;
   Item cur;
-  if (!next_item(k, cur)) return;
+  if (!next_item(k, cur)) {
+    store_edges();
+    return;
+  }
   int kv_end = kv_end_of(cur);
   __amdgpu_buffer_rsrc_t rs = rsrc_of(cur, kv_end);
 
@@ -426,6 +525,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
       }
     }
 
+    if (STORE) {
+      KArgs* sa = sargs();
+#pragma unroll
+      for (int i = 0; i < NI; ++i) own_load(sa, cur, i, csl[i], ck[i], cv[i]);
+    }
+
     // The next item's Q and first K/V tile go out before this item's
     // epilogue, so their latency overlaps the normalisation and stores.
     Item nxt;
@@ -449,8 +554,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     // each 32-key sub-tile), normalise, store.  The tile goes through LDS so
     // that each store instruction writes four whole 256-byte head rows (the
     // accumulator layout would scatter 8-byte pieces over 32 rows per store).
-    const float lt = l + __shfl_xor(l, 32);
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    float lt;
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+      lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    const float inv = lt > 0.f ? __builtin_amdgcn_rcpf(lt) : 0.f;
     __syncthreads();  // every wave is done with the ring (including the discarded look-ahead)
     u16* ob = lds + wave * (32 * OPITCH);  // this wave's 32 rows x 128 dims
 #pragma unroll
@@ -463,14 +572,29 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
         *reinterpret_cast<u32x2*>(ob + col * OPITCH + 32 * c + 8 * r + 4 * hl) = wv;
       }
     {
+      // All eight rows are read back before any store, and the stores go
+      // through a buffer resource that ends after the segment's last valid
+      // row, so rows past it are dropped without a branch per row.
       const int row0 = cur.qb * BQ + wq * 32;  // the wave's first query
-      u16* og = a.out + (int64_t)(cur.q_beg + row0) * a.o_stride + (cur.h * G + wh) * D + (lane & 15) * 8;
+      const int nrow = min(32, cur.Lq - row0);
+      u16* og = a.out + (int64_t)(cur.q_beg + row0) * a.o_stride + (cur.h * G + wh) * D;
+      const int ostep = (int)(a.o_stride * 2);
+      const __amdgpu_buffer_rsrc_t ors =
+          __builtin_amdgcn_make_buffer_rsrc(og, 0, nrow > 0 ? nrow * ostep : 0, 0x00020000);
+      u32x4 val[8];
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int r = 4 * it + (lane >> 4);
-        const u32x4 val = *reinterpret_cast<const u32x4*>(ob + r * OPITCH + (lane & 15) * 8);
-        if (row0 + r < cur.Lq) *reinterpret_cast<u32x4*>(og + (int64_t)r * a.o_stride) = val;
-      }
+      for (int it = 0; it < 8; ++it)
+        val[it] = *reinterpret_cast<const u32x4*>(ob + (4 * it + (lane >> 4)) * OPITCH + (lane & 15) * 8);
+      const int voff = (lane >> 4) * ostep + (lane & 15) * 16;
+#pragma unroll
+      for (int it = 0; it < 8; ++it)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val[it]), ors, voff, 4 * it * ostep, 0);
+    }
+    if (STORE) {
+      KArgs* sa = sargs();
+#pragma unroll
+      for (int i = 0; i < NI; ++i) own_store(sa, cur, csl[i], ck[i], cv[i]);
+      store_rest(cur);
     }
     if (!more) break;
     // Every wave has read its output rows back before the next item's tile 0
@@ -480,24 +604,25 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     k = kn;
     sc = prologue((kv_end + BKV - 1) / BKV);
   }
+  store_edges();
 }
 
-template <int G, bool CAUSAL, bool F16>
+template <int G, bool CAUSAL, bool F16, bool STORE>
 static void launch_t(Args a, int max_q, int n_cu, hipStream_t st) {
   constexpr int BQ = 32 * (kWaves / G);
   a.n_qblocks = (int)cdiv(max_q, BQ);
   const int64_t n_items = (int64_t)a.hkv * a.n_seqs * a.n_qblocks;
   const int grid = (int)std::min<int64_t>(n_items, n_cu);  // persistent: one workgroup per CU
-  hipLaunchKernelGGL((prefill_kernel<G, CAUSAL, F16>), dim3(grid), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL((prefill_kernel<G, CAUSAL, F16, STORE>), dim3(grid), dim3(kThreads), 0, st, a);
 }
 
-template <bool CAUSAL, bool F16>
+template <bool CAUSAL, bool F16, bool STORE = false>
 static int launch_g(const Args& a, int g, int max_q, int n_cu, hipStream_t st) {
   switch (g) {
-    case 1: launch_t<1, CAUSAL, F16>(a, max_q, n_cu, st); break;
-    case 2: launch_t<2, CAUSAL, F16>(a, max_q, n_cu, st); break;
-    case 4: launch_t<4, CAUSAL, F16>(a, max_q, n_cu, st); break;
-    case 8: launch_t<8, CAUSAL, F16>(a, max_q, n_cu, st); break;
+    case 1: launch_t<1, CAUSAL, F16, STORE>(a, max_q, n_cu, st); break;
+    case 2: launch_t<2, CAUSAL, F16, STORE>(a, max_q, n_cu, st); break;
+    case 4: launch_t<4, CAUSAL, F16, STORE>(a, max_q, n_cu, st); break;
+    case 8: launch_t<8, CAUSAL, F16, STORE>(a, max_q, n_cu, st); break;
     default: return AAC_ERR_UNSUPPORTED;
   }
   return AAC_OK;
@@ -534,7 +659,9 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
                           int32_t max_seqlen_k, int32_t n_q_heads, int32_t n_kv_heads,
                           int32_t head_dim, float scale, int32_t causal, void* out,
                           int64_t out_tok_stride, int32_t dtype, hipStream_t stream,
-                          bool launch) {
+                          bool launch, void* k_cache = nullptr, void* v_cache = nullptr,
+                          int64_t num_cache_rows = 0, const int64_t* slot_mapping = nullptr,
+                          int32_t n_store = 0) {
   if (dtype != AAC_DTYPE_BF16 && dtype != AAC_DTYPE_FP16) return AAC_ERR_UNSUPPORTED;
   if (head_dim != pf::D) return AAC_ERR_UNSUPPORTED;
   if (n_seqs < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_seqlen_q < 0 || max_seqlen_k < 0 ||
@@ -554,6 +681,8 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
   // staging uses 32-bit byte offsets within one segment's K/V rows
   if ((int64_t)max_seqlen_k * std::max(k_tok_stride, v_tok_stride) * 2 >= (int64_t(1) << 31))
     return AAC_ERR_UNSUPPORTED;
+  // the output stores use 32-bit byte offsets over a wave's 32 rows
+  if (out_tok_stride * 2 * 32 >= (int64_t(1) << 31)) return AAC_ERR_UNSUPPORTED;
   // work items (KV head, segment, 32-query block at most) are numbered in int32
   if ((int64_t)n_kv_heads * n_seqs * cdiv(max_seqlen_q, 32) >= (int64_t(1) << 30))
     return AAC_ERR_UNSUPPORTED;
@@ -574,11 +703,19 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
   a.scale_log2 = scale * kLog2e;
   a.out = (u16*)out;
   a.max_k = max_seqlen_k;
+  a.kc = (u16*)k_cache;
+  a.vc = (u16*)v_cache;
+  a.slots = slot_mapping;
+  a.num_rows = num_cache_rows;
+  a.n_tok = n_store;
   const bool f16 = dtype == AAC_DTYPE_FP16;
   int n_cu = 0;
   int rc = pf::device_cu_count(&n_cu);
   if (rc != AAC_OK) return rc;
-  if (causal)
+  if (n_store > 0)  // the store variant exists for causal attention only
+    rc = f16 ? pf::launch_g<true, true, true>(a, g, max_seqlen_q, n_cu, stream)
+             : pf::launch_g<true, false, true>(a, g, max_seqlen_q, n_cu, stream);
+  else if (causal)
     rc = f16 ? pf::launch_g<true, true>(a, g, max_seqlen_q, n_cu, stream)
              : pf::launch_g<true, false>(a, g, max_seqlen_q, n_cu, stream);
   else
@@ -629,6 +766,16 @@ extern "C" int aac_prefill_varlen_store(const void* q, const void* k, const void
   if (rc != AAC_OK) return rc;
   if (n_kv_tokens < 0 || num_cache_rows < 0) return AAC_ERR_INVALID_ARGUMENT;
   if (n_kv_tokens > 0 && (!k_cache || !v_cache || !slot_mapping)) return AAC_ERR_INVALID_ARGUMENT;
+  // Causal self-attention (one cu_seqlens array for queries and keys) stores
+  // inside the attention kernel; anything else stores first, then attends.
+  if (causal && cu_seqlens_q == cu_seqlens_k && max_seqlen_q == max_seqlen_k && n_seqs > 0 &&
+      max_seqlen_q > 0 && n_kv_tokens > 0 && n_kv_tokens < (int64_t(1) << 31) &&
+      ((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0)
+    return prefill_common(q, k, v, q_tok_stride, k_tok_stride, v_tok_stride, cu_seqlens_q,
+                          cu_seqlens_k, n_seqs, max_seqlen_q, max_seqlen_k, n_q_heads, n_kv_heads,
+                          head_dim, scale, causal, out, out_tok_stride, dtype,
+                          (hipStream_t)stream, true, k_cache, v_cache, num_cache_rows, slot_mapping,
+                          (int32_t)n_kv_tokens);
   rc = aac_kv_store(k, v, k_tok_stride, v_tok_stride, k_cache, v_cache, num_cache_rows, slot_mapping,
                     n_kv_tokens, n_kv_heads, head_dim, dtype, stream);
   if (rc != AAC_OK) return rc;

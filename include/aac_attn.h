@@ -125,10 +125,14 @@ int aac_prefill_varlen(const void* q, const void* k, const void* v, int64_t q_to
                        int64_t out_tok_stride, int32_t dtype, void* stream);
 
 /*
- * aac_kv_store(k, v -> caches via slot_mapping) followed by
+ * The result of aac_kv_store(k, v -> caches via slot_mapping) followed by
  * aac_prefill_varlen on the same stream: the whole per-layer attention block
  * of the reference's prefill (llm.py:171-184).  slot_mapping has n_kv_tokens
- * entries, one per packed key token (n_kv_tokens = cu_seqlens_k[n_seqs]).
+ * entries, one per packed key token (n_kv_tokens = cu_seqlens_k[n_seqs]);
+ * every one of them is stored, also tokens outside all segments.  Causal
+ * self-attention (cu_seqlens_q == cu_seqlens_k as pointers, equal max_seqlen)
+ * runs as one kernel that stores each q-block's K/V rows after attending to
+ * them; other calls launch the store, then the attention.
  */
 int aac_prefill_varlen_store(const void* q, const void* k, const void* v, int64_t q_tok_stride,
                              int64_t k_tok_stride, int64_t v_tok_stride,

@@ -213,3 +213,43 @@ def test_empty_sequences_and_understated_max_seqlen_k(gpu):
     absv = oracle.varlen_attention(f64(qv), kk[keep], np.abs(vv[keep]), cq.cpu().numpy(), ck_t,
                                    causal=False)
     check_attention(out, ref, what="clamped keys", absv=absv)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_store_in_the_attention_kernel_covers_every_token(gpu, hq, hkv, causal):
+    # One cu_seqlens array for queries and keys: the store runs inside the
+    # attention kernel, each work item writing its own q-block's K/V rows.
+    # Tokens before cu[0] and after cu[n], empty segments, padding slots (-1)
+    # and a max_seqlen below the longest segment (q-blocks no work item owns)
+    # must still be stored exactly as index_copy_ would.
+    print(f"case: store in the attention kernel hq={hq} hkv={hkv} causal={causal}", flush=True)
+    lens, lead, tail = [0, 37, 300, 1, 129, 0, 64], 3, 5
+    cu_np = (np.concatenate([[0], np.cumsum(lens)]) + lead).astype(np.int32)
+    N, d = lead + sum(lens) + tail, 128
+    g = torch.Generator(device=gpu).manual_seed(7)
+    qkv = torch.randn((N, (hq + 2 * hkv) * d), generator=g, device=gpu).to(torch.bfloat16)
+    q = qkv[:, :hq * d].view(N, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].contiguous().view(N, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(N, hkv, d)
+    cu = torch.from_numpy(cu_np).to(gpu)
+    rows = N + 40
+    rs = np.random.RandomState(hq + int(causal))
+    for max_len in (300, 100):
+        sm_np = rs.permutation(rows)[:N].astype(np.int64)
+        sm_np[rs.rand(N) < 0.1] = -1
+        kc = torch.randn((rows, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+        vc = torch.randn((rows, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+        kc_ref, vc_ref = np_of(kc).copy(), np_of(vc).copy()
+        out = fai.varlen_prefill_with_kvcache(q, k, v, cu, max_len, kc, vc,
+                                              torch.from_numpy(sm_np).to(gpu), causal=causal)
+        torch.cuda.synchronize()
+        oracle.kv_store(kc_ref, np_of(k), sm_np)
+        oracle.kv_store(vc_ref, np_of(v), sm_np)
+        assert np.array_equal(bytes_of(kc), kc_ref.view(np.uint8)), f"k cache, max_seqlen {max_len}"
+        assert np.array_equal(bytes_of(vc), vc_ref.view(np.uint8)), f"v cache, max_seqlen {max_len}"
+        if max_len >= max(lens):
+            a, b = int(cu_np[0]), int(cu_np[-1])
+            ref = oracle.varlen_attention(f64(q), f64(k), f64(v), cu_np, causal=causal)[a:b]
+            absv = oracle.varlen_attention(f64(q), f64(k), np.abs(f64(v)), cu_np, causal=causal)[a:b]
+            check_attention(out[a:b], ref, what="attention beside the store", absv=absv)
