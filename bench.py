@@ -36,7 +36,12 @@ Also reported on the same line:
                 single-threaded on the host cores.
 
 `python bench.py --gpus N --steps K --warmup W`; only N=1 is supported (one
-GPU), N>1 exits with a message.
+GPU), N>1 exits with a message.  Before its timed region every leg runs W
+warm-up iterations and then keeps its kernels running back to back for
+--warmup-seconds (default 1 s): the GPU's clocks fall while the host prepares
+a leg's inputs and climb back only under sustained load (8 x 1024 prefill:
+55 us right after an idle spell, 44 us after a few seconds of load), so the
+timed region measures the sustained rate a busy server sees.
 """
 from __future__ import annotations
 
@@ -71,6 +76,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup-seconds", type=float, default=1.0,
+                   help="back-to-back warm-up time per leg before its timed region")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--partition", type=int, default=0, help="decode partition tokens (0=auto)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -142,6 +149,18 @@ def launch_avg(torch, fn, n):
     return a.elapsed_time(b) / n / 1e3
 
 
+def warm(torch, fns, seconds):
+    """Run ``fns`` in turn back to back for ``seconds`` of wall time (untimed),
+    so the clocks reach their sustained level under this load."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            for fn in fns:
+                fn()
+        torch.cuda.synchronize()
+
+
 def bench_decode(torch, fai, dev, args, hq=16, hkv=8):
     x = make_decode_inputs(torch, dev, args.seed, hq=hq, hkv=hkv)
     attend_bytes, step_bytes = decode_bytes(x)
@@ -163,7 +182,7 @@ def bench_decode(torch, fai, dev, args, hq=16, hkv=8):
     for _ in range(args.warmup):
         step()
         attend()
-    torch.cuda.synchronize()
+    warm(torch, [step, attend], args.warmup_seconds)
     # whole step (store + attend), wall clock
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -195,6 +214,7 @@ def bench_decode_long(torch, fai, dev, args):
 
     for _ in range(args.warmup):
         attend()
+    warm(torch, [attend], args.warmup_seconds)
     t = launch_avg(torch, attend, args.steps)
     ach = attend_bytes / t / 1e9
     return {
@@ -225,6 +245,7 @@ def bench_kv_transfer(torch, dev, args):
     def timed(fn):
         for _ in range(args.warmup):
             fn()
+        warm(torch, [fn], args.warmup_seconds)
         return launch_avg(torch, fn, args.steps)
 
     t_ex = timed(lambda: kt.kv_export(st, bt, length, out=buf))
@@ -277,12 +298,8 @@ def bench_prefill(torch, fai, paged, dev, args, hq=16, hkv=8):
     for _ in range(args.warmup):
         step()
         attend()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t_step = (time.perf_counter() - t0) / args.steps
+    warm(torch, [step, attend], args.warmup_seconds)
+    t_step = launch_avg(torch, step, args.steps)
     t_att = launch_avg(torch, attend, args.steps)
     return dict(t_step=t_step, t_attend=t_att, flops=flops, tflops=flops / t_att / 1e12)
 
@@ -430,6 +447,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_seconds": args.warmup_seconds,
         "ms_per_step": round(dec["t_step"] * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
