@@ -215,20 +215,22 @@ def test_empty_sequences_and_understated_max_seqlen_k(gpu):
     check_attention(out, ref, what="clamped keys", absv=absv)
 
 
-@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8)])
+@pytest.mark.parametrize("hq,hkv,dtype", [(8, 8, torch.bfloat16), (16, 8, torch.bfloat16),
+                                           (32, 8, torch.bfloat16), (64, 8, torch.bfloat16),
+                                           (16, 8, torch.float16), (64, 8, torch.float16)])
 @pytest.mark.parametrize("causal", [True, False])
-def test_store_in_the_attention_kernel_covers_every_token(gpu, hq, hkv, causal):
+def test_store_in_the_attention_kernel_covers_every_token(gpu, hq, hkv, dtype, causal):
     # One cu_seqlens array for queries and keys: the store runs inside the
     # attention kernel, each work item writing its own q-block's K/V rows.
     # Tokens before cu[0] and after cu[n], empty segments, padding slots (-1)
     # and a max_seqlen below the longest segment (q-blocks no work item owns)
     # must still be stored exactly as index_copy_ would.
-    print(f"case: store in the attention kernel hq={hq} hkv={hkv} causal={causal}", flush=True)
+    print(f"case: store in the attention kernel hq={hq} hkv={hkv} {dtype} causal={causal}", flush=True)
     lens, lead, tail = [0, 37, 300, 1, 129, 0, 64], 3, 5
     cu_np = (np.concatenate([[0], np.cumsum(lens)]) + lead).astype(np.int32)
     N, d = lead + sum(lens) + tail, 128
     g = torch.Generator(device=gpu).manual_seed(7)
-    qkv = torch.randn((N, (hq + 2 * hkv) * d), generator=g, device=gpu).to(torch.bfloat16)
+    qkv = torch.randn((N, (hq + 2 * hkv) * d), generator=g, device=gpu).to(dtype)
     q = qkv[:, :hq * d].view(N, hq, d)
     k = qkv[:, hq * d:(hq + hkv) * d].contiguous().view(N, hkv, d)
     v = qkv[:, (hq + hkv) * d:].view(N, hkv, d)
@@ -238,8 +240,8 @@ def test_store_in_the_attention_kernel_covers_every_token(gpu, hq, hkv, causal):
     for max_len in (300, 100):
         sm_np = rs.permutation(rows)[:N].astype(np.int64)
         sm_np[rs.rand(N) < 0.1] = -1
-        kc = torch.randn((rows, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
-        vc = torch.randn((rows, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+        kc = torch.randn((rows, hkv, d), generator=g, device=gpu).to(dtype)
+        vc = torch.randn((rows, hkv, d), generator=g, device=gpu).to(dtype)
         kc_ref, vc_ref = np_of(kc).copy(), np_of(vc).copy()
         out = fai.varlen_prefill_with_kvcache(q, k, v, cu, max_len, kc, vc,
                                               torch.from_numpy(sm_np).to(gpu), causal=causal)
