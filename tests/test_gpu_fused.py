@@ -15,22 +15,37 @@ from awesome_acceleration_amd.qwen3 import Rope, rms_norm
 pytestmark = pytest.mark.gpu
 
 
-def ulp_close(a: torch.Tensor, b: torch.Tensor, what: str, max_frac: float = 2e-2):
+def ulp_close(a: torch.Tensor, b: torch.Tensor, what: str, max_frac: float = 2e-2,
+              scale: torch.Tensor | None = None):
     """Equal except for at most ``max_frac`` of the elements, each within a
     few units in the last place.  A one-ulp difference in the normalised value
     (fp32 summation order, correctly rounded vs. library rsqrt) can move a
     later rounded product or sum (x weight, x cos, + rotated term) by up to
     two ulps of the result; the bound allows four, relative to the larger
-    magnitude, plus the subnormal spacing."""
+    magnitude (or to ``scale``, the magnitude of the rounded terms a result
+    was summed from, where they can cancel), plus the subnormal spacing."""
     mant = 8 if a.dtype == torch.bfloat16 else 11  # significand bits
     tiny = 2.0 ** -133 if a.dtype == torch.bfloat16 else 2.0 ** -24
     a, b = a.float(), b.float()
     assert torch.isfinite(a).all(), what
-    tol = torch.maximum(a.abs(), b.abs()) * 2.0 ** -(mant - 3) + 4 * tiny
+    mag = torch.maximum(a.abs(), b.abs())
+    if scale is not None:
+        mag = torch.maximum(mag, scale.float())
+    tol = mag * 2.0 ** -(mant - 3) + 4 * tiny
     diff = (a - b).abs()
     assert (diff <= tol).all(), f"{what}: max diff {float(diff.max()):.3e}"
     frac = float((diff > 0).float().mean())
     assert frac <= max_frac, f"{what}: {frac:.4%} elements differ"
+
+
+def rope_terms(rope: Rope, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    """|x cos| + |rotate_half(x) sin|: the magnitude of the two rounded terms
+    each RoPE output is the sum of (they cancel where the output is small)."""
+    cos = rope.cos[positions].unsqueeze(1).float()
+    sin = rope.sin[positions].unsqueeze(1).float()
+    x = x.float()
+    x1, x2 = x[..., :rope.half], x[..., rope.half:]
+    return (x * cos).abs() + (torch.cat((-x2, x1), dim=-1) * sin).abs()
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -52,11 +67,15 @@ def test_rmsnorm_with_and_without_residual(gpu, dtype, hidden):
     ulp_close(fz.rmsnorm(wide[:, :hidden], w, 1e-6), rms_norm(wide[:, :hidden], w, 1e-6), "strided")
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8)])
-def test_qk_norm_rope_prefill_store(gpu, hq, hkv):
-    print(f"case: qk norm rope store {hq}/{hkv}", flush=True)
+@pytest.mark.parametrize("hq,hkv,T", [(16, 8, 777), (32, 8, 777), (8, 8, 777), (16, 8, 5000),
+                                      (32, 8, 4097)])
+def test_qk_norm_rope_prefill_store(gpu, hq, hkv, T):
+    # T >= 4096 takes the one-wavefront-per-token kernel, smaller T the
+    # one-row-per-(token, head) kernel
+    print(f"case: qk norm rope store {hq}/{hkv} T={T}", flush=True)
     g = torch.Generator(device=gpu).manual_seed(1)
-    T, D, bs, pool = 777, 128, 64, 20
+    D, bs = 128, 64
+    pool = -(-T // bs) + 8
     qkv = torch.randn((T, (hq + 2 * hkv) * D), generator=g, device=gpu).to(torch.bfloat16)
     qw = (1 + 0.3 * torch.randn(D, generator=g, device=gpu)).to(torch.bfloat16)
     kw = (1 + 0.3 * torch.randn(D, generator=g, device=gpu)).to(torch.bfloat16)
@@ -70,10 +89,10 @@ def test_qk_norm_rope_prefill_store(gpu, hq, hkv):
     q, k = fz.qk_norm_rope_store(qkv, hq, hkv, qw, kw, 1e-6, rope.cos, rope.sin, pos, kc, vc,
                                  slot_mapping=slots)
     torch.cuda.synchronize()
-    qr = rope.apply(rms_norm(qkv[:, :hq * D].view(T, hq, D), qw, 1e-6), pos)
-    kr = rope.apply(rms_norm(qkv[:, hq * D:(hq + hkv) * D].view(T, hkv, D), kw, 1e-6), pos)
-    ulp_close(q, qr, "q")
-    ulp_close(k, kr, "k")
+    qn = rms_norm(qkv[:, :hq * D].view(T, hq, D), qw, 1e-6)
+    kn = rms_norm(qkv[:, hq * D:(hq + hkv) * D].view(T, hkv, D), kw, 1e-6)
+    ulp_close(q, rope.apply(qn, pos), "q", scale=rope_terms(rope, qn, pos))
+    ulp_close(k, rope.apply(kn, pos), "k", scale=rope_terms(rope, kn, pos))
     v = qkv[:, (hq + hkv) * D:].view(T, hkv, D)
     keep = slots >= 0
     ek, ev = kc0.view(-1, hkv, D).clone(), vc0.view(-1, hkv, D).clone()
@@ -99,12 +118,13 @@ def test_qk_norm_rope_decode_append(gpu):
                                     vc, block_tables=bt, cache_seqlens=seqlens, want_k=False)
     torch.cuda.synchronize()
     assert none is None
-    kr = rope.apply(rms_norm(qkv[:, hq * D:(hq + hkv) * D].view(B, hkv, D), w1, 1e-6), seqlens)
+    kn = rms_norm(qkv[:, hq * D:(hq + hkv) * D].view(B, hkv, D), w1, 1e-6)
+    kr = rope.apply(kn, seqlens)
     v = qkv[:, (hq + hkv) * D:].view(B, hkv, D)
     btn, sl = bt.cpu().numpy(), seqlens.cpu().numpy()
     rows = torch.tensor([int(btn[b, sl[b] // bs]) * bs + int(sl[b]) % bs for b in range(B)],
                         device=gpu)
-    ulp_close(kc.view(-1, hkv, D)[rows], kr, "appended k")
+    ulp_close(kc.view(-1, hkv, D)[rows], kr, "appended k", scale=rope_terms(rope, kn, seqlens))
     assert torch.equal(vc.view(-1, hkv, D)[rows], v)
     assert int((kc.view(-1, hkv, D).abs().sum((1, 2)) > 0).sum()) == B  # nothing else written
 
