@@ -15,6 +15,9 @@ Also reported on the same line:
                 events on the launch stream around back-to-back launches,
                 divided by their count (every per-launch figure below is
                 timed the same way), against 8 TB/s HBM;
+  decode_slot   the same store+attend step through the reference's own cache
+                layout (slot caches [256, 2064, 8, 128] picked by
+                cache_batch_idx, as model/model.py:233-240 calls it);
   decode_long   long-context GQA-4 decode (64 sequences, 32 query / 8 KV heads,
                 context ~ U[16384, 32768]): the split-K decode plus its
                 log-sum-exp reduction, HIP events, against 8 TB/s HBM;
@@ -86,14 +89,15 @@ def parse():
     p.add_argument("--prefill-len", type=int, default=1024, help="tokens per segment (default 1024)")
     p.add_argument("--prefill-noncausal", action="store_true", help="prefill without the causal mask")
     p.add_argument("--no-long", action="store_true", help="skip the long-context GQA-4 decode leg")
+    p.add_argument("--no-slot", action="store_true", help="skip the slot-layout decode leg")
     p.add_argument("--no-kv", action="store_true", help="skip the KV export/import leg")
     p.add_argument("--no-tp2", action="store_true", help="skip the TP=2 per-rank shape leg")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine leg")
     p.add_argument("--e2e-seqs", type=int, default=256)
     p.add_argument("--e2e-in", type=int, default=1024)
     p.add_argument("--e2e-out", type=int, default=1024)
-    p.add_argument("--only", choices=["decode", "decode_long", "tp2_rank", "kv_transfer", "prefill",
-                                      "e2e"],
+    p.add_argument("--only", choices=["decode", "decode_slot", "decode_long", "tp2_rank", "kv_transfer",
+                                      "prefill", "e2e"],
                    default=None,
                    help="run one leg only (for profiling)")
     return p.parse_args()
@@ -195,6 +199,35 @@ def bench_decode(torch, fai, dev, args, hq=16, hkv=8):
     return dict(
         t_step=t_step, step_bytes=step_bytes, attend_bytes=attend_bytes, t_attend=t_att,
         achieved=achieved, x=x)
+
+
+# ----------------------------------------------------------------------------
+# the same decode through the reference's own slot layout: caches
+# [slots, max_seq_len, Hkv, D] picked by cache_batch_idx (model/model.py:233-240)
+# ----------------------------------------------------------------------------
+def bench_decode_slot(torch, fai, dev, args, lmax=2064):
+    x = make_decode_inputs(torch, dev, args.seed, bs=lmax)  # one block (slot) per sequence
+    attend_bytes, step_bytes = decode_bytes(x)
+    slots = x["bt_g"][:, 0].contiguous()
+
+    def step():  # the reference's call, store + attend
+        return fai.flash_attn_with_kvcache(
+            x["q"], x["kc"], x["vc"], k=x["kn"], v=x["vn"], cache_seqlens=x["seqlens_g"],
+            cache_batch_idx=slots, causal=False)
+
+    for _ in range(args.warmup):
+        step()
+    warm(torch, [step], args.warmup_seconds)
+    t = launch_avg(torch, step, args.steps)
+    ach = step_bytes / t / 1e9
+    return {
+        "workload": f"paged decode store+attend through flash_attn_with_kvcache(cache_batch_idx=...), "
+                    f"the reference's slot caches [256, {lmax}, 8, 128], 256 seqs, 16 q / 8 kv heads, "
+                    f"context U[1024,2047], shuffled slots",
+        "us_per_step": round(t * 1e6, 2),
+        "achieved": round(ach, 2), "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+        "bytes_per_step": step_bytes,
+    }
 
 
 # ----------------------------------------------------------------------------
@@ -401,6 +434,9 @@ def main():
     res = {}
     if args.only in (None, "decode"):
         res["decode"] = bench_decode(torch, fai, dev, args)
+    if args.only in (None, "decode_slot") and not args.no_slot:
+        res["decode_slot"] = bench_decode_slot(torch, fai, dev, args)
+        torch.cuda.empty_cache()
     if args.only in (None, "decode_long") and not args.no_long:
         res["decode_long"] = bench_decode_long(torch, fai, dev, args)
         torch.cuda.empty_cache()
@@ -488,6 +524,8 @@ def main():
         }
     if "decode_long" in res:
         line["decode_long"] = res["decode_long"]
+    if "decode_slot" in res:
+        line["decode_slot"] = res["decode_slot"]
     if "tp2_rank" in res:
         line["tp2_rank"] = res["tp2_rank"]
     if "kv_transfer" in res:
