@@ -79,6 +79,11 @@ struct DecodeArgs {
   int32_t n_parts;
   int32_t part_tokens;
   int32_t bs_shift;  // log2(block_size) when it is a power of two
+  // otherwise t / block_size = (t * bs_magic) >> bs_mshift for 0 <= t < 2^31
+  // (Granlund & Montgomery 1994, Thm 4.2: bs_magic = floor(2^(31+l) / d) + 1
+  // with l = ceil(log2 d), bs_mshift = 31 + l)
+  uint64_t bs_magic;
+  int32_t bs_mshift;
   int32_t lpt;       // 1: blockIdx.z is a rank in descending context order
   int32_t lpt_max;   // context bound the length classes are scaled to
 };
@@ -273,7 +278,9 @@ __global__ __launch_bounds__(256, G <= 2 ? 4 : 2) void decode_paged_kernel(Decod
   // Token t of this partition, or t0 (a valid token whose row is finite and
   // whose probability is set to 0) past its end, so loads never branch.
   auto token = [&](int t) { return t < t1 ? t : t0; };
-  auto block_index = [&](int t) { return POW2 ? t >> a.bs_shift : t / a.block_size; };
+  auto block_index = [&](int t) {
+    return POW2 ? t >> a.bs_shift : (int)(((uint64_t)(uint32_t)t * a.bs_magic) >> a.bs_mshift);
+  };
   // The block numbers of an iteration's U tokens are loaded one iteration
   // ahead: a block-table load waited for right before the K/V loads would,
   // with in-order load counters, also wait for every K/V load issued before
@@ -609,6 +616,14 @@ static int decode_common(const void* q, int64_t q_seq_stride, const void* k_cach
   a.n_parts = plan.n_parts;
   a.part_tokens = plan.part_tokens;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  if (a.bs_shift < 0) {  // block_size >= 3 here
+    const int l = 32 - __builtin_clz((unsigned)(block_size - 1));
+    a.bs_magic = (uint64_t(1) << (31 + l)) / (uint64_t)block_size + 1;
+    a.bs_mshift = 31 + l;
+  } else {
+    a.bs_magic = 0;
+    a.bs_mshift = 0;
+  }
   // length order only without a split: split partitions are already
   // uniform work units, and the ordering costs every workgroup a few barriers
   a.lpt = plan.n_parts == 1 && n_seqs >= 2 && n_seqs <= kLptMaxSeqs;
