@@ -36,7 +36,10 @@ Also reported on the same line:
                 token) and total tok/s (prompt + generated), as
                 benchmark_tp.py:93-99 defines them;
   cpu_baseline  the numpy oracle on a bounded sample of the decode workload,
-                single-threaded on the host cores.
+                single-threaded on the host cores; e2e.cpu_baseline is the
+                end-to-end decode step on the host (one decoder layer for all
+                256 sequences in fp32 torch on up to 16 host threads, times 28
+                layers, plus lm_head) as output tok/s beside the GPU's.
 
 `python bench.py --gpus N --steps K --warmup W`; only N=1 is supported (one
 GPU), N>1 exits with a message.  Before its timed region every leg runs W
@@ -418,6 +421,89 @@ def cpu_baseline(x, reps=12, seed=1):
                 seconds_per_step=round(med, 3))
 
 
+def cpu_e2e_baseline(torch, ctx, threads, reps=3, seed=2, hidden=1024, inter=3072, hq=16, hkv=8,
+                     d=128, layers=28, vocab=151936, theta=1e6, eps=1e-6):
+    """The end-to-end decode step on the host: one Qwen3 decoder layer
+    (model/model.py:202-267: RMSNorm, fused QKV, q/k RMSNorm, RoPE, the K/V
+    append into the reference's slot caches, GQA attention over each
+    sequence's context, o_proj, residual, RMSNorm, SiLU-gated MLP, residual)
+    for all sequences at once in fp32 torch on ``threads`` host threads, the
+    median of ``reps`` runs, times the number of layers, plus the tied lm_head
+    projection and argmax: output tok/s = sequences / step time."""
+    import torch.nn.functional as F
+    from awesome_acceleration_amd.qwen3 import rms_norm
+
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        g = torch.Generator().manual_seed(seed)
+        B, lmax = int(ctx.shape[0]), int(ctx.max())
+        rnd = lambda *shape, s=1.0: torch.randn(*shape, generator=g) * s
+        w = dict(ln1=1 + rnd(hidden, s=0.1), ln2=1 + rnd(hidden, s=0.1), qn=1 + rnd(d, s=0.1),
+                 kn=1 + rnd(d, s=0.1), qkv=rnd((hq + 2 * hkv) * d, hidden, s=0.02),
+                 o=rnd(hidden, hq * d, s=0.02), gu=rnd(2 * inter, hidden, s=0.02),
+                 down=rnd(hidden, inter, s=0.02))
+        base = torch.randn(1 << 22, generator=g).to(torch.bfloat16)
+
+        def filled(*shape):  # random bf16 rows, a 4 Mi-element draw repeated (fast to fill)
+            t = torch.empty(*shape, dtype=torch.bfloat16)
+            flat = t.view(-1)
+            for i in range(0, flat.numel(), base.numel()):
+                flat[i:i + base.numel()] = base[:min(base.numel(), flat.numel() - i)]
+            return t
+
+        kc = filled(B, lmax, hkv, d)  # slot caches (model/model.py:328-335)
+        vc = filled(B, lmax, hkv, d)
+        x = rnd(B, hidden)
+        pos = torch.from_numpy(ctx.astype(np.int64) - 1)  # the new token's position
+        inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+        ang = torch.cat((torch.outer(pos.float(), inv),) * 2, dim=-1)
+        cos, sin = ang.cos().unsqueeze(1), ang.sin().unsqueeze(1)
+
+        def rope(t):
+            t1, t2 = t[..., :d // 2], t[..., d // 2:]
+            return t * cos + torch.cat((-t2, t1), dim=-1) * sin
+
+        def layer(x):
+            h = rms_norm(x, w["ln1"], eps)
+            qkv = F.linear(h, w["qkv"])
+            q = rope(rms_norm(qkv[:, :hq * d].view(B, hq, d), w["qn"], eps))
+            k = rope(rms_norm(qkv[:, hq * d:(hq + hkv) * d].view(B, hkv, d), w["kn"], eps))
+            v = qkv[:, (hq + hkv) * d:].view(B, hkv, d)
+            att = torch.empty(B, hq, d)
+            for b in range(B):
+                n = int(ctx[b])
+                kc[b, n - 1], vc[b, n - 1] = k[b].to(torch.bfloat16), v[b].to(torch.bfloat16)
+                kb = kc[b, :n].float().permute(1, 2, 0)          # [hkv, d, n]
+                vb = vc[b, :n].float().permute(1, 0, 2)          # [hkv, n, d]
+                sb = torch.matmul(q[b].view(hkv, hq // hkv, d), kb) * d ** -0.5
+                att[b] = torch.matmul(torch.softmax(sb, dim=-1), vb).reshape(hq, d)
+            x = x + F.linear(att.reshape(B, hq * d), w["o"])
+            gu = F.linear(rms_norm(x, w["ln2"], eps), w["gu"])
+            return x + F.linear(F.silu(gu[:, :inter]) * gu[:, inter:], w["down"])
+
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            layer(x)
+            times.append(time.perf_counter() - t0)
+        t_layer = float(np.median(times))
+        del kc, vc
+        embed = rnd(vocab, hidden, s=0.02)
+        t0 = time.perf_counter()
+        F.linear(rms_norm(x, w["ln1"], eps), embed).argmax(-1)
+        t_head = time.perf_counter() - t0
+    finally:
+        torch.set_num_threads(prev)
+    step = layers * t_layer + t_head
+    return dict(value=round(B / step, 2), unit="output tok/s", cores=threads, kind="port",
+                sample=f"one decoder layer's decode step for {B} sequences (context "
+                       f"{int(ctx.min())}-{int(ctx.max())}, slot caches) in fp32 torch on "
+                       f"{threads} host threads, median of {reps} runs ({t_layer:.3f} s), times "
+                       f"{layers} layers, plus the lm_head projection and argmax ({t_head:.3f} s)",
+                seconds_per_step=round(step, 3))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -534,6 +620,11 @@ def main():
         line["e2e"] = res["e2e"]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(dec["x"])
+        if "e2e" in line:  # the end-to-end decode step on the host, same contexts
+            line["e2e"]["cpu_baseline"] = cpu_e2e_baseline(
+                torch, dec["x"]["ctx"], threads=min(len(os.sched_getaffinity(0)), 16))
+            line["e2e"]["vs_cpu"] = round(line["e2e"]["output_tok_s"] /
+                                          line["e2e"]["cpu_baseline"]["value"], 1)
     print(json.dumps(line))
 
 

@@ -35,3 +35,12 @@ def test_cpu_baseline_reports_a_port_on_one_core():
     assert r["kind"] == "port" and r["cores"] == 1 and r["unit"] == "GB/s"
     assert r["value"] > 0 and r["seconds_per_step"] >= 0
     assert "3 sequences (306 context tokens)" in r["sample"]
+
+
+def test_cpu_e2e_baseline_runs_the_layer_on_the_host():
+    import torch
+    ctx = np.array([3, 40, 17], np.int32)
+    r = bench.cpu_e2e_baseline(torch, ctx, threads=2, reps=1, hidden=64, inter=96, hq=4, hkv=2,
+                               d=16, layers=2, vocab=50)
+    assert r["unit"] == "output tok/s" and r["kind"] == "port" and r["cores"] == 2
+    assert r["value"] > 0 and "3 sequences (context 3-40" in r["sample"]
