@@ -30,6 +30,8 @@ Also reported on the same line:
   prefill       varlen causal prefill, 8 x 1024 tokens, 16/8 heads, bf16, with
                 the paged store in the same call, as TFLOP/s against the
                 2.5 PFLOP/s dense bf16 MFMA peak (roofline of that kernel);
+  prefill_long  the same kernel on 8 x 8192 causal tokens: its steady-state
+                rate, where per-item start and epilogue costs are small;
   e2e           random-init Qwen3-0.6B, 256 requests x 1024 input / 1024
                 output tokens under the continuous-batching engine: output
                 tok/s (generated tokens / wall clock from submit to the last
@@ -93,6 +95,7 @@ def parse():
     p.add_argument("--prefill-noncausal", action="store_true", help="prefill without the causal mask")
     p.add_argument("--no-long", action="store_true", help="skip the long-context GQA-4 decode leg")
     p.add_argument("--no-slot", action="store_true", help="skip the slot-layout decode leg")
+    p.add_argument("--no-prefill-long", action="store_true", help="skip the 8 x 8192 prefill leg")
     p.add_argument("--no-kv", action="store_true", help="skip the KV export/import leg")
     p.add_argument("--no-tp2", action="store_true", help="skip the TP=2 per-rank shape leg")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine leg")
@@ -100,7 +103,7 @@ def parse():
     p.add_argument("--e2e-in", type=int, default=1024)
     p.add_argument("--e2e-out", type=int, default=1024)
     p.add_argument("--only", choices=["decode", "decode_slot", "decode_long", "tp2_rank", "kv_transfer",
-                                      "prefill", "e2e"],
+                                      "prefill", "prefill_long", "e2e"],
                    default=None,
                    help="run one leg only (for profiling)")
     return p.parse_args()
@@ -340,6 +343,36 @@ def bench_prefill(torch, fai, paged, dev, args, hq=16, hkv=8):
     return dict(t_step=t_step, t_attend=t_att, flops=flops, tflops=flops / t_att / 1e12)
 
 
+def bench_prefill_long(torch, fai, dev, args, nseq=8, L=8192, hq=16, hkv=8):
+    """The same kernel on long segments (8 x 8192 causal), where the per-item
+    start and epilogue costs are small against the tile loop: the kernel's
+    steady-state rate."""
+    d, N = 128, nseq * L
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    qkv = torch.randn((N, (hq + 2 * hkv) * d), generator=g, device=dev).to(torch.bfloat16)
+    q = qkv[:, :hq * d].view(N, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].contiguous().view(N, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(N, hkv, d)
+    cu = torch.arange(0, N + 1, L, dtype=torch.int32, device=dev)
+    flops = 4 * hq * d * nseq * (L * (L + 1) // 2)
+
+    def attend():
+        return fai.flash_attn_varlen_func(q, k, v, cu, cu, L, L, causal=True)
+
+    for _ in range(3):
+        attend()
+    warm(torch, [attend], args.warmup_seconds)
+    t = launch_avg(torch, attend, max(5, args.steps // 5))
+    ach = flops / t / 1e12
+    return {
+        "workload": f"varlen causal prefill {nseq} x {L} tokens, {hq}/{hkv} heads, head_dim 128, bf16",
+        "us_attend": round(t * 1e6, 2),
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+                     "flops_per_launch": flops, "traffic": None},
+    }
+
+
 # ----------------------------------------------------------------------------
 # end to end: random-init Qwen3-0.6B under the continuous-batching engine
 # ----------------------------------------------------------------------------
@@ -547,6 +580,9 @@ def main():
         res["kv_transfer"] = bench_kv_transfer(torch, dev, args)
     if args.only in (None, "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, fai, paged, dev, args)
+    if args.only in (None, "prefill_long") and not args.no_prefill_long:
+        res["prefill_long"] = bench_prefill_long(torch, fai, dev, args)
+        torch.cuda.empty_cache()
     if args.only in (None, "e2e") and not args.no_e2e:
         res["e2e"] = bench_e2e(torch, args)
     if args.only is not None:
@@ -612,6 +648,8 @@ def main():
         line["decode_long"] = res["decode_long"]
     if "decode_slot" in res:
         line["decode_slot"] = res["decode_slot"]
+    if "prefill_long" in res:
+        line["prefill_long"] = res["prefill_long"]
     if "tp2_rank" in res:
         line["tp2_rank"] = res["tp2_rank"]
     if "kv_transfer" in res:
