@@ -61,6 +61,8 @@ SIGNATURES: dict[str, tuple] = {
          _p, _p, _i32, _p, _i32, _i32, _p],
     ),
     "aac_silu_mul": (_c_int, [_p, _p, _i64, _i32, _i32, _p]),
+    "aac_gemm_nt": (
+        _c_int, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
     "aac_kv_export_paged": (
         _c_int, [_p, _i64, _i64, _i32, _i64, _i32, _i32, _i32, _p, _i32, _i32, _p, _i32, _p]),
     "aac_kv_import_paged": (

@@ -1,0 +1,306 @@
+// Decode-batch projection GEMM (gfx950, bf16/fp16 MFMA): Y = X W^T with X the
+// [M, K] activations of one decode step (M = running sequences, at most a few
+// hundred) and W a torch Linear weight [N, K] -- the QKV, o_proj, gate_up and
+// down projections of the Qwen3 layer (model/model.py:132-154, :180-190).
+// With `silu_intermediate` = I the weight is the fused [gate | up] projection
+// [2I, K] and the epilogue writes silu(gate) * up [M, I] (model/model.py:190),
+// rounded where the unfused torch expression rounds.
+//
+// Why a hand-written kernel: at M = 256 these GEMMs are weight-streaming
+// bound (QKV: 8 MiB of weights against 2.1 GFLOP), and the library's tiles for
+// this shape leave most CUs idle while a few stream long K ranges.  Here the
+// output is cut into tiles so that every CU gets one (or a few), each
+// workgroup stages its X and W rows through LDS with coalesced 16-byte loads
+// kept several stages deep in registers, and the K range of a tile can be
+// split over the workgroup's four waves (reduced through LDS at the end).
+//
+// Tiling: a workgroup is 4 waves; wave (wm, wn, ks) owns the 32 x 32 output
+// block (rows 32 wm, columns 32 wn) for the K slice ks of every staged stage.
+// MW x NW x KS = 4.  One stage holds KT = 64 KF KS columns of K (each wave
+// takes 64 KF of them: 4 KF MFMA steps) for the workgroup's 32 MW X rows and
+// 32 NW (x2 with the gate/up pairing) W rows.
+// The MFMA computes D = W_blk X_blk^T (v_mfma_f32_32x32x16: A = 32 W rows x 16
+// k, B = 16 k x 32 X rows), so a lane ends with one token (column of D) and
+// 4 runs of 4 consecutive output features: 8-byte stores.
+//
+// Tiles are numbered so that the M-tiles of one N-tile are consecutive and
+// land on one XCD (workgroups are dealt round-robin over the 8 XCDs), so a
+// W tile is fetched from HBM once per XCD and re-read from that XCD's L2.
+
+#include "aac_common.h"
+
+namespace aac {
+namespace gm {
+
+struct Args {
+  const u16* x;
+  const u16* w;
+  u16* y;
+  int64_t x_stride, w_stride, y_stride;  // row strides (elements)
+  int32_t m, k;
+  int32_t n_tiles;   // tiles along the output columns
+  int32_t silu_off;  // gate/up pairing: W row of up column 0 (= I)
+};
+
+template <bool F16> struct Mma;
+template <> struct Mma<false> {
+  __device__ static inline f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline float round(float f) { return bf16lo(f32_to_bf16_bits(f)); }
+  __device__ static inline u32 pack(float a, float b) { return pack_bf16x2(a, b); }
+};
+template <> struct Mma<true> {
+  __device__ static inline f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline float round(float f) { return (float)(_Float16)f; }
+  __device__ static inline u32 pack(float a, float b) { return pack_f16x2(a, b); }
+};
+
+template <int MW, int NW, int KS, int KF, bool SILU, bool F16, int PD>
+__global__ __launch_bounds__(256) void gemm_kernel(Args a) {
+  constexpr int NB = SILU ? 2 : 1;        // accumulators per wave (gate, up)
+  constexpr int MT = 32 * MW;             // X rows per tile
+  constexpr int WT = 32 * NW * NB;        // W rows per tile
+  constexpr int R = MT + WT;              // staged rows
+  constexpr int KW = 64 * KF;             // K per wave per stage (4 KF MFMA steps)
+  constexpr int KT = KW * KS;             // K per stage
+  constexpr int C = KT / 8;               // 16-byte chunks per staged row
+  constexpr int PITCH = KT + 8;           // LDS row pitch (elements): conflict-free b128 reads
+  constexpr int RS = 256 / C;             // rows covered by one pass of the 256 threads
+  constexpr int CH = R / RS;              // 16-byte chunks per thread per stage
+  constexpr int CX = MT / RS;             // ... of which X chunks
+  constexpr int kBuf = R * PITCH;
+  static_assert(MW * NW * KS == 4, "four waves");
+  static_assert(R % RS == 0 && MT % RS == 0, "whole passes");
+  static_assert((KS - 1) * MW * NW * NB * 16 * 64 * 4 <= 2 * kBuf * 2, "reduction fits");
+  typedef Mma<F16> M;
+
+  __shared__ __attribute__((aligned(16))) u16 lds[2 * kBuf];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % MW, wn = (wave / MW) % NW, ks = wave / (MW * NW);
+
+  const int n_mt = (a.m + MT - 1) / MT;
+  const int T = n_mt * a.n_tiles;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  const int mt = t % n_mt, nt = t / n_mt;
+  const int m0 = mt * MT, n0 = nt * 32 * NW;  // first token / output column
+
+  // staging sources: thread chunk i covers row RS*i + tid/C, 16 bytes at
+  // column 8*(tid % C) of the stage
+  const int sr = tid / C, sc = (tid % C) * 8;
+  const u16* src[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int r = RS * i + sr;
+    if (i < CX) {
+      src[i] = a.x + (int64_t)min(m0 + r, a.m - 1) * a.x_stride + sc;  // past-the-end rows clamp
+    } else {
+      const int wr = r - MT;
+      const int row = SILU && wr >= 32 * NW ? a.silu_off + n0 + wr - 32 * NW : n0 + wr;
+      src[i] = a.w + (int64_t)row * a.w_stride + sc;
+    }
+  }
+  const int st_off = sr * PITCH + sc;
+
+  const int nk = a.k / KT;
+  u32x4 pre[PD][CH];
+  auto load = [&](u32x4* p, int stage) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) p[i] = *reinterpret_cast<const u32x4*>(src[i] + stage * KT);
+  };
+  auto write = [&](u16* buf, const u32x4* p) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) *reinterpret_cast<u32x4*>(buf + st_off + RS * i * PITCH) = p[i];
+  };
+
+  f32x16 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[nb][i] = 0.f;
+
+  // fragment reads: lane = (row l%32, 8 k at 8*(l/32)) of the wave's blocks
+  const int fx = (32 * wm + (lane & 31)) * PITCH + KW * ks + 8 * (lane >> 5);
+  const int fw = (MT + 32 * wn + (lane & 31)) * PITCH + KW * ks + 8 * (lane >> 5);
+  auto compute = [&](const u16* buf) {
+#pragma unroll
+    for (int s = 0; s < 4 * KF; ++s) {
+      const u32x4 bx = *reinterpret_cast<const u32x4*>(buf + fx + 16 * s);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const u32x4 aw = *reinterpret_cast<const u32x4*>(buf + fw + nb * 32 * NW * PITCH + 16 * s);
+        acc[nb] = M::run(aw, bx, acc[nb]);
+      }
+    }
+  };
+
+  // Stage kk goes registers -> LDS buffer kk&1, then a barrier, then the
+  // MFMAs read it.  The buffer's previous readers (stage kk-2) finished before
+  // the barrier of stage kk-1.  Loads run PD stages ahead; every stage of the
+  // main loop issues its refill (the stage index clamped to the last one), so
+  // the number of loads in flight, and the wait before each LDS write, is the
+  // same on every path.
+#pragma unroll
+  for (int s = 0; s < PD; ++s) load(pre[s], min(s, nk - 1));
+  int kk = 0;
+  for (; kk + PD <= nk; kk += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+      u16* buf = lds + ((kk + u) & 1) * kBuf;
+      write(buf, pre[u]);
+      load(pre[u], min(kk + u + PD, nk - 1));
+      __syncthreads();
+      compute(buf);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < PD - 1; ++u) {  // the last nk % PD stages
+    if (kk + u < nk) {
+      u16* buf = lds + ((kk + u) & 1) * kBuf;
+      write(buf, pre[u]);
+      __syncthreads();
+      compute(buf);
+    }
+  }
+
+  // K-split waves hand their partial sums to the ks = 0 wave of their block
+  if (KS > 1) {
+    float* red = reinterpret_cast<float*>(lds);
+    const int slot = wm + MW * wn;
+    __syncthreads();  // every wave is done with the stage buffers
+    if (ks > 0) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          red[((((ks - 1) * MW * NW + slot) * NB + nb) * 16 + i) * 64 + lane] = acc[nb][i];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int j = 0; j < KS - 1; ++j)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[nb][i] += red[(((j * MW * NW + slot) * NB + nb) * 16 + i) * 64 + lane];
+  }
+
+  const int m = m0 + 32 * wm + (lane & 31);
+  if (m >= a.m) return;
+  u16* yr = a.y + (int64_t)m * a.y_stride + n0 + 32 * wn + 4 * (lane >> 5);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (SILU) {
+        // torch rounds the gate_up product, then F.silu, then the product
+        const float gt = M::round(acc[0][4 * g + j]);
+        const float up = M::round(acc[NB - 1][4 * g + j]);
+        const float s = M::round(gt / (1.f + __expf(-gt)));
+        v[j] = s * up;
+      } else {
+        v[j] = acc[0][4 * g + j];
+      }
+    }
+    u32x2 o;
+    o[0] = M::pack(v[0], v[1]);
+    o[1] = M::pack(v[2], v[3]);
+    *reinterpret_cast<u32x2*>(yr + 8 * g) = o;
+  }
+}
+
+template <int MW, int NW, int KS, int KF, bool SILU, bool F16>
+static void launch_t(Args a, int n_out, hipStream_t st) {
+  constexpr int PD = 3;  // stages in flight (2 to 6 measured alike; 3 no slower)
+  a.n_tiles = n_out / (32 * NW);
+  const int grid = (int)cdiv(a.m, 32 * MW) * a.n_tiles;
+  hipLaunchKernelGGL((gemm_kernel<MW, NW, KS, KF, SILU, F16, PD>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <bool SILU, bool F16>
+static int launch_c(const Args& a, int cfg, int n_out, hipStream_t st) {
+  switch (cfg) {
+    case 1: launch_t<2, 2, 1, 2, SILU, F16>(a, n_out, st); break;
+    case 2: launch_t<1, 1, 4, 1, SILU, F16>(a, n_out, st); break;
+    case 3: launch_t<2, 1, 2, 1, SILU, F16>(a, n_out, st); break;
+    case 4: launch_t<1, 2, 2, 1, SILU, F16>(a, n_out, st); break;
+    default: return AAC_ERR_INVALID_ARGUMENT;
+  }
+  return AAC_OK;
+}
+
+// (MW, NW, K per stage) of each configuration id
+static const int kCfg[5][3] = {{0, 0, 0}, {2, 2, 128}, {1, 1, 256}, {2, 1, 128}, {1, 2, 128}};
+
+// The configuration for a shape: the fewest K splits whose tile count fills
+// the GPU (>= 256 tiles), else the one with the most tiles.
+static int pick_config(int m, int n_out, int k) {
+  const int order[4] = {1, 3, 4, 2};
+  int best = 0;
+  int64_t best_tiles = -1;
+  for (int c : order) {
+    const int tc = 32 * kCfg[c][1];
+    if (n_out % tc || k % kCfg[c][2]) continue;
+    const int64_t tiles = cdiv(m, 32 * kCfg[c][0]) * (n_out / tc);
+    if (tiles >= 256) return c;
+    if (tiles > best_tiles) {
+      best_tiles = tiles;
+      best = c;
+    }
+  }
+  return best;
+}
+
+}  // namespace gm
+}  // namespace aac
+
+using namespace aac;
+
+extern "C" int aac_gemm_nt(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
+                           void* y, int64_t y_row_stride, int32_t m, int32_t n, int32_t k,
+                           int32_t silu_intermediate, int32_t config, int32_t dtype, void* stream) {
+  if (dtype != AAC_DTYPE_BF16 && dtype != AAC_DTYPE_FP16) return AAC_ERR_UNSUPPORTED;
+  if (m < 0 || n <= 0 || k <= 0 || silu_intermediate < 0 || config < 0 || config > 4)
+    return AAC_ERR_INVALID_ARGUMENT;
+  const bool silu = silu_intermediate > 0;
+  if (silu && silu_intermediate != n) return AAC_ERR_SHAPE;  // n = I output columns
+  if (x_row_stride < k || w_row_stride < k || y_row_stride < n) return AAC_ERR_SHAPE;
+  if (m == 0) return AAC_OK;
+  if (!x || !w || !y) return AAC_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)x | (uintptr_t)w) % 16 || (uintptr_t)y % 8 || x_row_stride % 8 ||
+      w_row_stride % 8 || y_row_stride % 4)
+    return AAC_ERR_MISALIGNED;
+  const int cfg = config ? config : gm::pick_config(m, n, k);
+  if (cfg == 0) return AAC_ERR_UNSUPPORTED;
+  const int tc = 32 * gm::kCfg[cfg][1];
+  if (n % tc || k % gm::kCfg[cfg][2]) return AAC_ERR_UNSUPPORTED;
+  if (cdiv(m, 32 * gm::kCfg[cfg][0]) * (n / tc) >= (int64_t(1) << 31)) return AAC_ERR_UNSUPPORTED;
+  gm::Args a;
+  a.x = (const u16*)x;
+  a.w = (const u16*)w;
+  a.y = (u16*)y;
+  a.x_stride = x_row_stride;
+  a.w_stride = w_row_stride;
+  a.y_stride = y_row_stride;
+  a.m = m;
+  a.k = k;
+  a.silu_off = silu_intermediate;
+  a.n_tiles = 0;
+  const hipStream_t st = (hipStream_t)stream;
+  int rc;
+  if (dtype == AAC_DTYPE_FP16)
+    rc = silu ? gm::launch_c<true, true>(a, cfg, n, st) : gm::launch_c<false, true>(a, cfg, n, st);
+  else
+    rc = silu ? gm::launch_c<true, false>(a, cfg, n, st) : gm::launch_c<false, false>(a, cfg, n, st);
+  if (rc != AAC_OK) return rc;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AAC_OK : (int)e;
+}

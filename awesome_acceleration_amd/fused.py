@@ -9,7 +9,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["rmsnorm", "qk_norm_rope_store", "silu_mul"]
+__all__ = ["rmsnorm", "qk_norm_rope_store", "silu_mul", "linear", "linear_supported"]
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -96,6 +96,31 @@ def qk_norm_rope_store(qkv: torch.Tensor, n_q_heads: int, n_kv_heads: int,
         _code(qkv), _stream(qkv))
     _lib.check(rc, "aac_qk_norm_rope_store")
     return q, k
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, silu: bool = False,
+           config: int = 0) -> torch.Tensor:
+    """``F.linear(x, weight)`` for a decode step's small ``x`` [m, k]; with
+    ``silu`` the weight is the fused [gate | up] projection [2I, k] and the
+    result is ``silu(gate) * up`` [m, I] (model/model.py:190)."""
+    _req(x.is_cuda and x.dim() == 2 and x.stride(1) == 1, "x must be a [m, k] GPU tensor")
+    _req(weight.dim() == 2 and weight.stride(1) == 1 and weight.dtype == x.dtype,
+         "weight must be [n, k] with contiguous rows, same dtype as x")
+    m, k = x.shape
+    _req(weight.shape[1] == k, "inner dimensions differ")
+    n = weight.shape[0] // 2 if silu else weight.shape[0]
+    _req(not silu or weight.shape[0] == 2 * n, "gate/up weight must have an even row count")
+    y = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    rc = _lib.lib().aac_gemm_nt(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                                y.data_ptr(), y.stride(0), m, n, k, n if silu else 0, config,
+                                _code(x), _stream(x))
+    _lib.check(rc, "aac_gemm_nt")
+    return y
+
+
+def linear_supported(m: int, n: int, k: int) -> bool:
+    """Whether aac_gemm_nt has a tiling for this shape."""
+    return m > 0 and ((n % 64 == 0 and k % 64 == 0) or (n % 32 == 0 and k % 128 == 0))
 
 
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:

@@ -161,7 +161,14 @@ class Qwen3ForCausalLM:
         self.q_size = self.hq * self.d
         self.kv_size = self.hkv * self.d
         self.scale = self.d ** -0.5
+        # decode steps up to this many sequences use the decode-batch GEMM
+        # (its tiles assume a few hundred rows at most)
+        self.small_gemm_rows = 512
         self.init_weights(seed)
+        H, I = cfg.hidden_size, cfg.intermediate_size
+        if not all(fz.linear_supported(1, n, k) for n, k in (
+                (self.q_size + 2 * self.kv_size, H), (H, self.q_size), (I, H), (H, I))):
+            self.small_gemm_rows = 0  # a shape the decode-batch GEMM has no tiling for
         self.rope = Rope(self.d, cfg.max_position_embeddings, cfg.rope_theta, self.device, dtype)
 
     @torch.no_grad()
@@ -237,19 +244,24 @@ class Qwen3ForCausalLM:
     def _forward_fused(self, input_ids, meta: StepMeta, cache: PagedKVCache, prefill: bool):
         """The same layer with the fused call-site kernels: residual add +
         RMSNorm, q/k RMSNorm + RoPE + KV store/append, SiLU * up are one launch
-        each, and the residual add of each block is folded into the next norm."""
+        each, and the residual add of each block is folded into the next norm.
+        A decode step's projections (one row per sequence) run on the
+        decode-batch GEMM, gate/up with SiLU * up in its epilogue; prefill
+        steps (many rows) keep the library GEMMs."""
         eps = self.cfg.rms_norm_eps
         I = self.cfg.intermediate_size
         h = F.embedding(input_ids, self.embed)
         res, delta = h, None
         T = h.shape[0]
         pos = meta.positions if meta.positions.dtype == torch.int32 else meta.positions.int()
+        small = not prefill and T <= self.small_gemm_rows
+        lin = fz.linear if small else F.linear
         for li, L in enumerate(self.layers):
             if delta is None:
                 x = fz.rmsnorm(res, L["ln1"], eps)
             else:
                 x, res = fz.rmsnorm(delta, L["ln1"], eps, residual=res)
-            qkv = F.linear(x, L["qkv"])
+            qkv = lin(x, L["qkv"])
             if prefill:
                 q, k = fz.qk_norm_rope_store(
                     qkv, self.hq, self.hkv, L["q_norm"], L["k_norm"], eps, self.rope.cos,
@@ -266,9 +278,12 @@ class Qwen3ForCausalLM:
                 attn = fai.decode_paged(q, cache.k(li), cache.v(li), meta.block_tables,
                                         meta.context_lens, softmax_scale=self.scale,
                                         max_context_len=meta.max_context_len)
-            o = F.linear(attn.reshape(T, -1), L["o"])
+            o = lin(attn.reshape(T, -1), L["o"])
             x, res = fz.rmsnorm(o, L["ln2"], eps, residual=res)
-            delta = F.linear(fz.silu_mul(F.linear(x, L["gate_up"])), L["down"])
+            if small:
+                delta = fz.linear(fz.linear(x, L["gate_up"], silu=True), L["down"])
+            else:
+                delta = F.linear(fz.silu_mul(F.linear(x, L["gate_up"])), L["down"])
         if prefill:
             delta, res = delta[meta.last_idx], res[meta.last_idx]
         h, _ = fz.rmsnorm(delta, self.norm, eps, residual=res)

@@ -248,6 +248,25 @@ int aac_silu_mul(const void* gate_up, void* out, int64_t n_rows, int32_t interme
                  int32_t dtype, void* stream);
 
 /*
+ * Decode-batch projection: y[m, n] = sum_k x[m, k] * w[n, k] (torch's
+ * F.linear(x, w), fp32 accumulation, rounded to dtype) for x [m, k] and a
+ * Linear weight w [n, k], rows strided by *_row_stride elements.  With
+ * silu_intermediate = I (> 0) the weight is the fused [gate | up] projection
+ * [2I, k], n must equal I, and y[m, i] = dtype(silu(dtype(gate))) *
+ * dtype(up), the rounding of act_fn(gate_proj(x)) * up_proj(x)
+ * (model/model.py:190) -- the product of aac_silu_mul without the [m, 2I]
+ * intermediate.  Built for shapes where n is a multiple of 32 and k of 64
+ * (of 128 / 256 for some tilings); config 0 lets the library pick the tiling,
+ * 1..4 force one (tuning).  Meant for the small m of a decode step (tens to
+ * hundreds of rows): every output tile is one workgroup.
+ * Replaces the q/k/v, o_proj, gate/up and down nn.Linear calls of the
+ * decoder layer (model/model.py:132-154, :180-190) on decode steps.
+ */
+int aac_gemm_nt(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, void* y,
+                int64_t y_row_stride, int32_t m, int32_t n, int32_t k, int32_t silu_intermediate,
+                int32_t config, int32_t dtype, void* stream);
+
+/*
  * KV export: gather the first `length` tokens of one sequence from a paged
  * cache into a contiguous buffer out[n_layers][2][length][Hkv][D] (index 0 =
  * K, 1 = V).  Layer l's K cache starts at kv_cache + l * layer_stride and its
