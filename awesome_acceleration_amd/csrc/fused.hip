@@ -7,7 +7,7 @@
 //   q/k RMSNorm + RoPE       model/model.py:225-228 (rotation in the
 //                            activation dtype, model/model.py:86-99)
 //   KV store / append        llm.py:171-174, model/model.py:233-240
-//   SiLU(gate) * up          model/model.py:190
+//   SiLU(gate) * up          model/model.py:188
 // Here each chain is one launch.  Every value is rounded to the activation
 // dtype at the same points as the torch expression it replaces, so the fused
 // results equal the unfused ones up to fp32 summation order inside the norm.

@@ -1,9 +1,9 @@
 // Decode-batch projection GEMM (gfx950, bf16/fp16 MFMA): Y = X W^T with X the
 // [M, K] activations of one decode step (M = running sequences, at most a few
 // hundred) and W a torch Linear weight [N, K] -- the QKV, o_proj, gate_up and
-// down projections of the Qwen3 layer (model/model.py:132-154, :180-190).
+// down projections of the Qwen3 layer (model/model.py:132-154, :258, :178-188).
 // With `silu_intermediate` = I the weight is the fused [gate | up] projection
-// [2I, K] and the epilogue writes silu(gate) * up [M, I] (model/model.py:190),
+// [2I, K] and the epilogue writes silu(gate) * up [M, I] (model/model.py:188),
 // rounded where the unfused torch expression rounds.
 //
 // Why a hand-written kernel: at M = 256 these GEMMs are weight-streaming

@@ -102,7 +102,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, silu: bool = False,
            config: int = 0) -> torch.Tensor:
     """``F.linear(x, weight)`` for a decode step's small ``x`` [m, k]; with
     ``silu`` the weight is the fused [gate | up] projection [2I, k] and the
-    result is ``silu(gate) * up`` [m, I] (model/model.py:190)."""
+    result is ``silu(gate) * up`` [m, I] (model/model.py:188)."""
     _req(x.is_cuda and x.dim() == 2 and x.stride(1) == 1, "x must be a [m, k] GPU tensor")
     _req(weight.dim() == 2 and weight.stride(1) == 1 and weight.dtype == x.dtype,
          "weight must be [n, k] with contiguous rows, same dtype as x")
@@ -124,7 +124,7 @@ def linear_supported(m: int, n: int, k: int) -> bool:
 
 
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
-    """``silu(gate) * up`` of the fused [gate | up] projection (model/model.py:190)."""
+    """``silu(gate) * up`` of the fused [gate | up] projection (model/model.py:188)."""
     _req(gate_up.is_cuda and gate_up.dim() == 2 and gate_up.is_contiguous(), "gate_up [rows, 2I]")
     rows, two_i = gate_up.shape
     out = torch.empty((rows, two_i // 2), dtype=gate_up.dtype, device=gate_up.device)

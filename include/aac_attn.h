@@ -242,7 +242,7 @@ int aac_qk_norm_rope_store(const void* qkv, int64_t qkv_tok_stride, int64_t n_to
 /*
  * out[r, i] = dtype(silu(gate_up[r, i])) * gate_up[r, intermediate + i] for the
  * fused [gate | up] projection gate_up [n_rows, 2*intermediate].
- * Replaces act_fn(gate_proj(x)) * up_proj(x) (model/model.py:190).
+ * Replaces act_fn(gate_proj(x)) * up_proj(x) (model/model.py:188).
  */
 int aac_silu_mul(const void* gate_up, void* out, int64_t n_rows, int32_t intermediate,
                  int32_t dtype, void* stream);
@@ -254,13 +254,13 @@ int aac_silu_mul(const void* gate_up, void* out, int64_t n_rows, int32_t interme
  * silu_intermediate = I (> 0) the weight is the fused [gate | up] projection
  * [2I, k], n must equal I, and y[m, i] = dtype(silu(dtype(gate))) *
  * dtype(up), the rounding of act_fn(gate_proj(x)) * up_proj(x)
- * (model/model.py:190) -- the product of aac_silu_mul without the [m, 2I]
+ * (model/model.py:188) -- the product of aac_silu_mul without the [m, 2I]
  * intermediate.  Built for shapes where n is a multiple of 32 and k of 64
  * (of 128 / 256 for some tilings); config 0 lets the library pick the tiling,
  * 1..4 force one (tuning).  Meant for the small m of a decode step (tens to
  * hundreds of rows): every output tile is one workgroup.
  * Replaces the q/k/v, o_proj, gate/up and down nn.Linear calls of the
- * decoder layer (model/model.py:132-154, :180-190) on decode steps.
+ * decoder layer (model/model.py:132-154, :258, :178-188) on decode steps.
  */
 int aac_gemm_nt(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, void* y,
                 int64_t y_row_stride, int32_t m, int32_t n, int32_t k, int32_t silu_intermediate,

@@ -1,7 +1,7 @@
 """Fused call-site kernels against the reference's own torch expressions:
 RMSNorm (model/model.py:47-52) with the residual add before it, q/k RMSNorm +
 RoPE (model/model.py:86-99, :225-228) with the KV store (llm.py:171-174) or
-decode append, and SiLU * up (model/model.py:190).  The fused kernels round at
+decode append, and SiLU * up (model/model.py:188).  The fused kernels round at
 the same points, so results match to one unit in the last place where fp32
 summation order differs, and the cache stores are bit-exact."""
 import numpy as np

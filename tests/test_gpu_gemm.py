@@ -1,13 +1,13 @@
 """Decode-batch projection GEMM (aac_gemm_nt) against an fp32 reference.
 
 y = x w^T (torch's F.linear for the q/k/v, o_proj, gate/up and down
-projections, model/model.py:132-154, :180-190) is checked against the same
+projections, model/model.py:132-154, :258, :178-188) is checked against the same
 product in fp32 on the bf16 inputs: the kernel accumulates in fp32 in its own
 order and rounds once, so every element is within one rounding of the exact
 value (2^-8 relative, with margin for the fp32 summation).  The gate/up
 variant is checked against the reference expression evaluated from the fp32
 products rounded to the activation dtype, act_fn(gate) * up
-(model/model.py:190): elements whose rounded gate or up differ from the
+(model/model.py:188): elements whose rounded gate or up differ from the
 kernel's by the fp32 summation order may move by a few ulps."""
 import pytest
 import torch
