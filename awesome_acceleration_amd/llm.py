@@ -72,6 +72,7 @@ class _Seq:
     blocks: list[int]
     tokens: list[int]        # generated so far
     pos: int                 # position of the next token to feed
+    done: bool = False       # finished (a step launched ahead may still hold its row)
 
 
 class LLM:
@@ -105,10 +106,15 @@ class LLM:
         self.allocator.allocate(1)
         self.use_graphs = use_graphs
         self._graphs: dict[int, tuple] = {}
-        # packed per-step host metadata: ids | positions | seqlens | ctx | tables
+        # packed per-step host metadata: ids | positions | seqlens | ctx | tables | live
+        # (live = 1 for a sequence's row, 0 for a graph padding row)
         W = self.blocks_per_seq
-        self._host = torch.zeros(max_num_seqs * (4 + W), dtype=torch.int32, pin_memory=True)
-        self._dev = torch.zeros(max_num_seqs * (4 + W), dtype=torch.int32, device=self.device)
+        self._host = torch.zeros(max_num_seqs * (5 + W), dtype=torch.int32, pin_memory=True)
+        self._dev = torch.zeros(max_num_seqs * (5 + W), dtype=torch.int32, device=self.device)
+        # sampled ids of a decode step launched ahead, read back without a sync
+        self._tok_host = [torch.zeros(max_num_seqs, dtype=torch.int32, pin_memory=True)
+                          for _ in range(2)]
+        self._tok_turn = 0
         self._request_queue: queue.Queue[_Request] = queue.Queue()
         self._loop_running = False
         self._loop_thread: Optional[threading.Thread] = None
@@ -187,20 +193,20 @@ class LLM:
         the scratch block 0 at position 0 and their logits are dropped.
         """
         n, W = len(seqs), self.blocks_per_seq
-        B = min(1 << (n - 1).bit_length(), self.max_num_seqs) if self.use_graphs else n
+        B = self._bucket(n)
         h = self._host.numpy()
-        h[:4 * B + B * W] = 0
+        h[:5 * B + B * W] = 0
         h[:n] = [s.tokens[-1] for s in seqs]
         h[B:B + n] = [s.pos for s in seqs]
-        h[2 * B:2 * B + n] = [s.pos for s in seqs]  # tokens already in the cache
+        h[2 * B:2 * B + n] = h[B:B + n]              # tokens already in the cache
         h[3 * B:4 * B] = h[2 * B:3 * B] + 1           # context after the append
         tab = h[4 * B:4 * B + B * W].reshape(B, W)
         for i, s in enumerate(seqs):
             tab[i, :len(s.blocks)] = s.blocks
-        m = B * (4 + W)
+        h[4 * B + B * W:4 * B + B * W + n] = 1        # live rows
+        m = B * (5 + W)
         self._dev[:m].copy_(self._host[:m], non_blocking=True)
         self.stats["decode_steps"] += 1
-        self.stats["decode_tokens"] += n
         if not self.use_graphs:
             meta = self._decode_meta(B, self.blocks_per_seq * self.block_size)
             return self.model.forward(self._dev[:B], meta, self.cache, prefill=False)
@@ -209,6 +215,44 @@ class LLM:
             g = self._capture(B)
         g[0].replay()
         return g[1][:n]
+
+    def _bucket(self, n: int) -> int:
+        return min(1 << (n - 1).bit_length(), self.max_num_seqs) if self.use_graphs else n
+
+    def _sample_ahead(self, n: int, temperature: float):
+        """After a graph step of n sequences: sample every row on the device,
+        make the samples the next step's input ids, advance the live rows'
+        positions and cache lengths by one (the device-side state of the
+        next step, whose block tables are unchanged: blocks are reserved at
+        admission), and copy the samples to pinned host memory.  Returns the
+        handle ``_tokens`` waits on."""
+        B, W = self._bucket(n), self.blocks_per_seq
+        logits = self._graphs[B][1]
+        if temperature == 0:
+            tok = logits.argmax(dim=-1)
+        else:
+            tok = torch.multinomial(torch.softmax(logits.float() / temperature, dim=-1), 1)
+            tok = tok.squeeze(-1)
+        d = self._dev
+        d[:B].copy_(tok)
+        d[B:4 * B].view(3, B).add_(d[4 * B + B * W:5 * B + B * W].view(1, B))
+        buf = self._tok_host[self._tok_turn]
+        self._tok_turn ^= 1
+        buf[:B].copy_(d[:B], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        return n, ev, buf
+
+    def _step_ahead(self, n: int):
+        """Replay the graph of the last batch from the device-side state."""
+        self.stats["decode_steps"] += 1
+        self._graphs[self._bucket(n)][0].replay()
+
+    @staticmethod
+    def _tokens(handle) -> list[int]:
+        n, ev, buf = handle
+        ev.synchronize()
+        return buf[:n].tolist()
 
     def _capture(self, B: int):
         """Capture one decode step of batch B as a HIP graph.  Every launch
@@ -232,6 +276,7 @@ class LLM:
     # ------------------------------------------------------------ the loop
     def _finish(self, s: _Seq, free_rows: list[int]):
         req = s.req
+        s.done = True
         text = self.decode_fn(s.tokens) if self.decode_fn else ""
         req.results[s.prompt_idx] = GenerationOutput(
             text, list(s.tokens), len(req.token_ids[s.prompt_idx]), len(s.tokens))
@@ -239,6 +284,22 @@ class LLM:
         bisect.insort(free_rows, s.row)
         if all(r is not None for r in req.results):
             req.future.set_result(req.results)
+
+    def _retire(self, seqs: list[_Seq], sampled: list[int], active: dict, free_rows: list[int]) -> bool:
+        """Phase 5 for one decode step: append each live sequence's token and
+        finish those that stop.  Returns whether any sequence finished."""
+        finished = False
+        for s, tok in zip(seqs, sampled):
+            if s.done:  # finished after an earlier step; this row's token is dropped
+                continue
+            s.tokens.append(tok)
+            s.pos += 1
+            self.stats["decode_tokens"] += 1
+            if self._should_stop(s, tok):
+                del active[s.row]
+                self._finish(s, free_rows)
+                finished = True
+        return finished
 
     def _should_stop(self, s: _Seq, tok: int) -> bool:
         return (len(s.tokens) >= s.req.max_tokens or s.pos >= self.max_seq_len
@@ -292,14 +353,33 @@ class LLM:
                     continue
                 # Phase 4: one decode step for every active sequence
                 seqs = [active[r] for r in sorted(active)]
-                sampled = self._sample(self._decode_step(seqs), seqs[0].req.temperature)
-                # Phase 5: bookkeeping
-                for s, tok in zip(seqs, sampled):
-                    s.tokens.append(tok)
-                    s.pos += 1
-                    if self._should_stop(s, tok):
-                        del active[s.row]
-                        self._finish(s, free_rows)
+                temp = seqs[0].req.temperature
+                if not self.use_graphs:
+                    self._retire(seqs, self._sample(self._decode_step(seqs), temp), active,
+                                 free_rows)  # Phase 5: bookkeeping
+                    continue
+                # With graphs the next step of the same batch is launched from
+                # the device-side state before the host reads this step's
+                # tokens, so the bookkeeping and the next launch overlap the
+                # GPU.  A row that finishes computes one discarded token in
+                # the step launched ahead (into its own blocks, before they
+                # can be handed to a later prefill on the same stream); the
+                # batch is rebuilt on the host once rows finish or a waiting
+                # request may be admitted.
+                self._decode_step(seqs)
+                h = self._sample_ahead(len(seqs), temp)
+                while True:
+                    ahead = None
+                    if self._request_queue.empty() and (not pending or not free_rows):
+                        self._step_ahead(len(seqs))
+                        ahead = self._sample_ahead(len(seqs), temp)
+                    finished = self._retire(seqs, self._tokens(h), active, free_rows)
+                    if ahead is None:
+                        break
+                    h = ahead
+                    if finished or not self._loop_running:
+                        self._retire(seqs, self._tokens(h), active, free_rows)
+                        break
         except BaseException as e:  # surface failures to every waiting caller
             for s in active.values():
                 if not s.req.future.done():
