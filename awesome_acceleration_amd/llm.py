@@ -20,6 +20,11 @@ Changes on the hot path:
   per-layer host synchronisation (the reference syncs in RoPE,
   model/model.py:82, and writes decode inputs element by element,
   llm.py:395-398).
+* With HIP graphs, a decode step of an unchanged batch is launched from the
+  device-side state the previous step left (sampled ids as the next input,
+  positions and cache lengths advanced in place) before the host reads the
+  previous step's tokens, so the host's bookkeeping overlaps the GPU; the
+  reference's loop syncs on every step's tokens (llm.py:404-405, :413-443).
 * No tokenizer is available offline, so prompts are token-id lists and
   ``GenerationOutput.text`` is empty unless a ``decode_fn`` is supplied.
 """
