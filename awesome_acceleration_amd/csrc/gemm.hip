@@ -12,11 +12,11 @@
 // output is cut into tiles so that every CU gets one (or a few), each
 // workgroup stages its X and W rows through LDS with coalesced 16-byte loads
 // kept several stages deep in registers, and the K range of a tile can be
-// split over the workgroup's four waves (reduced through LDS at the end).
+// split over the workgroup's waves (reduced through LDS at the end).
 //
-// Tiling: a workgroup is 4 waves; wave (wm, wn, ks) owns the 32 x 32 output
-// block (rows 32 wm, columns 32 wn) for the K slice ks of every staged stage.
-// MW x NW x KS = 4.  One stage holds KT = 64 KF KS columns of K (each wave
+// Tiling: a workgroup is 4 or 8 waves; wave (wm, wn, ks) owns the 32 x 32
+// output block (rows 32 wm, columns 32 wn) for the K slice ks of every staged
+// stage.  MW x NW x KS = 4 or 8.  One stage holds KT = 64 KF KS columns of K (each wave
 // takes 64 KF of them: 4 KF MFMA steps) for the workgroup's 32 MW X rows and
 // 32 NW (x2 with the gate/up pairing) W rows.
 // The MFMA computes D = W_blk X_blk^T (v_mfma_f32_32x32x16: A = 32 W rows x 16
@@ -61,7 +61,7 @@ template <> struct Mma<true> {
 };
 
 template <int MW, int NW, int KS, int KF, bool SILU, bool F16, int PD>
-__global__ __launch_bounds__(256) void gemm_kernel(Args a) {
+__global__ __launch_bounds__(64 * MW * NW * KS) void gemm_kernel(Args a) {
   constexpr int NB = SILU ? 2 : 1;        // accumulators per wave (gate, up)
   constexpr int MT = 32 * MW;             // X rows per tile
   constexpr int WT = 32 * NW * NB;        // W rows per tile
@@ -70,11 +70,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(Args a) {
   constexpr int KT = KW * KS;             // K per stage
   constexpr int C = KT / 8;               // 16-byte chunks per staged row
   constexpr int PITCH = KT + 8;           // LDS row pitch (elements): conflict-free b128 reads
-  constexpr int RS = 256 / C;             // rows covered by one pass of the 256 threads
+  constexpr int NT = 64 * MW * NW * KS;   // threads
+  constexpr int RS = NT / C;              // rows covered by one pass of the threads
   constexpr int CH = R / RS;              // 16-byte chunks per thread per stage
   constexpr int CX = MT / RS;             // ... of which X chunks
   constexpr int kBuf = R * PITCH;
-  static_assert(MW * NW * KS == 4, "four waves");
+  static_assert(MW * NW * KS == 4 || MW * NW * KS == 8, "four or eight waves");
   static_assert(R % RS == 0 && MT % RS == 0, "whole passes");
   static_assert((KS - 1) * MW * NW * NB * 16 * 64 * 4 <= 2 * kBuf * 2, "reduction fits");
   typedef Mma<F16> M;
@@ -218,31 +219,49 @@ __global__ __launch_bounds__(256) void gemm_kernel(Args a) {
 }
 
 template <int MW, int NW, int KS, int KF, bool SILU, bool F16>
-static void launch_t(Args a, int n_out, hipStream_t st) {
+static int launch_t(Args a, int n_out, hipStream_t st) {
   constexpr int PD = 3;  // stages in flight (2 to 6 measured alike; 3 no slower)
-  a.n_tiles = n_out / (32 * NW);
-  const int grid = (int)cdiv(a.m, 32 * MW) * a.n_tiles;
-  hipLaunchKernelGGL((gemm_kernel<MW, NW, KS, KF, SILU, F16, PD>), dim3(grid), dim3(256), 0, st, a);
+  constexpr int lds_bytes = 2 * (32 * MW + 32 * NW * (SILU ? 2 : 1)) * (64 * KF * KS + 8) * 2;
+  if constexpr (lds_bytes > 160 * 1024) {
+    return AAC_ERR_UNSUPPORTED;  // the gate/up pairing does not fit LDS at this stage size
+  } else {
+    a.n_tiles = n_out / (32 * NW);
+    const int grid = (int)cdiv(a.m, 32 * MW) * a.n_tiles;
+    hipLaunchKernelGGL((gemm_kernel<MW, NW, KS, KF, SILU, F16, PD>), dim3(grid),
+                       dim3(64 * MW * NW * KS), 0, st, a);
+    return AAC_OK;
+  }
 }
 
 template <bool SILU, bool F16>
 static int launch_c(const Args& a, int cfg, int n_out, hipStream_t st) {
   switch (cfg) {
-    case 1: launch_t<2, 2, 1, 2, SILU, F16>(a, n_out, st); break;
-    case 2: launch_t<1, 1, 4, 1, SILU, F16>(a, n_out, st); break;
-    case 3: launch_t<2, 1, 2, 1, SILU, F16>(a, n_out, st); break;
-    case 4: launch_t<1, 2, 2, 1, SILU, F16>(a, n_out, st); break;
+    case 1: return launch_t<2, 2, 1, 2, SILU, F16>(a, n_out, st);
+    case 2: return launch_t<1, 1, 4, 1, SILU, F16>(a, n_out, st);
+    case 3: return launch_t<2, 1, 2, 1, SILU, F16>(a, n_out, st);
+    case 4: return launch_t<1, 2, 2, 1, SILU, F16>(a, n_out, st);
+    case 5: return launch_t<2, 2, 2, 2, SILU, F16>(a, n_out, st);
+    case 6: return launch_t<1, 1, 8, 1, SILU, F16>(a, n_out, st);
+    case 7: return launch_t<2, 1, 4, 1, SILU, F16>(a, n_out, st);
+    case 8: return launch_t<2, 2, 2, 1, SILU, F16>(a, n_out, st);
     default: return AAC_ERR_INVALID_ARGUMENT;
   }
-  return AAC_OK;
 }
 
 // (MW, NW, K per stage) of each configuration id
-static const int kCfg[5][3] = {{0, 0, 0}, {2, 2, 128}, {1, 1, 256}, {2, 1, 128}, {1, 2, 128}};
+static const int kCfg[9][3] = {{0, 0, 0},    {2, 2, 128}, {1, 1, 256}, {2, 1, 128}, {1, 2, 128},
+                               {2, 2, 256}, {1, 1, 512}, {2, 1, 256}, {2, 2, 128}};
 
-// The configuration for a shape: the fewest K splits whose tile count fills
-// the GPU (>= 256 tiles), else the one with the most tiles.
+// The configuration for a shape.  Measured at m = 256 (the Qwen3-0.6B decode
+// projections, HIP-graph replay, cold weights): 64 x 64 tiles on 8 waves
+// (K split over two, config 8) are the fastest tiling once there are 128 or
+// more of them (QKV 6.7 us, gate/up + SiLU 12.8 us); with fewer, 32 x 32
+// tiles with K split over 4 waves (config 2: o_proj 6.7 us, down 8.7 us).
+// Otherwise: the fewest K splits whose tile count fills the GPU (>= 256
+// tiles), else the tiling with the most tiles.
 static int pick_config(int m, int n_out, int k) {
+  if (n_out % 64 == 0 && k % 128 == 0 && cdiv(m, 64) * (n_out / 64) >= 128) return 8;
+  if (n_out % 32 == 0 && k % 256 == 0 && cdiv(m, 32) * (n_out / 32) >= 256) return 2;
   const int order[4] = {1, 3, 4, 2};
   int best = 0;
   int64_t best_tiles = -1;
@@ -268,7 +287,7 @@ extern "C" int aac_gemm_nt(const void* x, int64_t x_row_stride, const void* w, i
                            void* y, int64_t y_row_stride, int32_t m, int32_t n, int32_t k,
                            int32_t silu_intermediate, int32_t config, int32_t dtype, void* stream) {
   if (dtype != AAC_DTYPE_BF16 && dtype != AAC_DTYPE_FP16) return AAC_ERR_UNSUPPORTED;
-  if (m < 0 || n <= 0 || k <= 0 || silu_intermediate < 0 || config < 0 || config > 4)
+  if (m < 0 || n <= 0 || k <= 0 || silu_intermediate < 0 || config < 0 || config > 8)
     return AAC_ERR_INVALID_ARGUMENT;
   const bool silu = silu_intermediate > 0;
   if (silu && silu_intermediate != n) return AAC_ERR_SHAPE;  // n = I output columns

@@ -53,7 +53,7 @@ def test_linear_matches_fp32_reference(gpu, m, n, k, dtype):
     _check_linear(y, x, w, f"{m}x{n}x{k} {dtype}")
 
 
-@pytest.mark.parametrize("config", [1, 2, 3, 4])
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_every_tiling(gpu, config):
     """Each forced tiling on a shape all of them support, with strided rows."""
     m, n, k = 200, 512, 1024
@@ -76,7 +76,7 @@ def _silu_ref(x, w):
 @pytest.mark.parametrize("m,i,k,config", [
     (256, 3072, 1024, 0),  # gate/up of a Qwen3-0.6B decode step
     (256, 3072, 1024, 1), (256, 3072, 1024, 2), (256, 3072, 1024, 4),
-    (200, 3072, 1024, 3), (37, 3072, 1024, 0),
+    (200, 3072, 1024, 3), (37, 3072, 1024, 0), (256, 3072, 1024, 7), (100, 3072, 1024, 8),
     (5, 3072, 1024, 0), (130, 256, 512, 0),
 ])
 def test_silu_gate_up_matches_reference(gpu, m, i, k, config, dtype):
