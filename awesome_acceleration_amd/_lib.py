@@ -63,6 +63,10 @@ SIGNATURES: dict[str, tuple] = {
     "aac_silu_mul": (_c_int, [_p, _p, _i64, _i32, _i32, _p]),
     "aac_gemm_nt": (
         _c_int, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
+    "aac_qkv_norm_rope_store": (
+        _c_int,
+        [_p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p, _f32, _p, _p, _i32, _p, _p, _p,
+         _p, _p, _i64, _p, _p, _i32, _p, _i32, _i32, _p]),
     "aac_kv_export_paged": (
         _c_int, [_p, _i64, _i64, _i32, _i64, _i32, _i32, _i32, _p, _i32, _i32, _p, _i32, _p]),
     "aac_kv_import_paged": (

@@ -27,7 +27,7 @@
 // land on one XCD (workgroups are dealt round-robin over the 8 XCDs), so a
 // W tile is fetched from HBM once per XCD and re-read from that XCD's L2.
 
-#include "aac_common.h"
+#include "qk_head.h"
 
 namespace aac {
 namespace gm {
@@ -40,6 +40,7 @@ struct Args {
   int32_t m, k;
   int32_t n_tiles;   // tiles along the output columns
   int32_t silu_off;  // gate/up pairing: W row of up column 0 (= I)
+  fz::QkArgs qk;     // QKV epilogue: q/k norm + RoPE, q out, K/V to the cache
 };
 
 template <bool F16> struct Mma;
@@ -60,7 +61,7 @@ template <> struct Mma<true> {
   __device__ static inline u32 pack(float a, float b) { return pack_f16x2(a, b); }
 };
 
-template <int MW, int NW, int KS, int KF, bool SILU, bool F16, int PD>
+template <int MW, int NW, int KS, int KF, bool SILU, bool F16, int PD, bool QK = false>
 __global__ __launch_bounds__(64 * MW * NW * KS) void gemm_kernel(Args a) {
   constexpr int NB = SILU ? 2 : 1;        // accumulators per wave (gate, up)
   constexpr int MT = 32 * MW;             // X rows per tile
@@ -184,13 +185,56 @@ __global__ __launch_bounds__(64 * MW * NW * KS) void gemm_kernel(Args a) {
           red[((((ks - 1) * MW * NW + slot) * NB + nb) * 16 + i) * 64 + lane] = acc[nb][i];
     }
     __syncthreads();
-    if (ks > 0) return;
+    if (ks == 0) {
 #pragma unroll
-    for (int j = 0; j < KS - 1; ++j)
+      for (int j = 0; j < KS - 1; ++j)
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[nb][i] += red[(((j * MW * NW + slot) * NB + nb) * 16 + i) * 64 + lane];
+          for (int i = 0; i < 16; ++i)
+            acc[nb][i] += red[(((j * MW * NW + slot) * NB + nb) * 16 + i) * 64 + lane];
+    } else if (!QK) {
+      return;
+    }
+  }
+
+  if constexpr (QK) {
+    // The tile is one head (128 columns) of 32 tokens: the ks = 0 waves write
+    // it, rounded, to LDS (after the reduction's floats), then each of the
+    // 32 DPP rows of the 8 waves takes one token and runs the per-head q/k
+    // RMSNorm + RoPE + store of the fused call-site kernel on it.
+    static_assert(MW == 1 && NW == 4 && KS == 2 && !SILU, "one head of 32 tokens on 8 waves");
+    constexpr int TP = 128 + 8;  // tile row pitch (elements)
+    constexpr int kRedElems = 2 * (KS - 1) * MW * NW * 16 * 64;  // the floats, in u16 units
+    static_assert(kRedElems + 32 * TP <= 2 * kBuf, "tile fits");
+    u16* tile = lds + kRedElems;
+    if (ks == 0) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32x2 o;
+        o[0] = M::pack(acc[0][4 * g], acc[0][4 * g + 1]);
+        o[1] = M::pack(acc[0][4 * g + 2], acc[0][4 * g + 3]);
+        *reinterpret_cast<u32x2*>(tile + (lane & 31) * TP + 32 * wn + 8 * g + 4 * (lane >> 5)) = o;
+      }
+    }
+    __syncthreads();
+    constexpr Dt DT = F16 ? Dt::FP16 : Dt::BF16;
+    const fz::QkArgs& q = a.qk;
+    const int r = wave * 4 + (lane >> 4), li = lane & 15;  // token row, 8 dims at 8 li
+    const int64_t t = m0 + r;
+    if (t >= a.m) return;  // the whole 16-lane row
+    const u32x4 xr = *reinterpret_cast<const u32x4*>(tile + r * TP + li * 8);
+    const int hh = nt;  // head of this tile: q heads, then k heads, then v heads
+    const int64_t crow = fz::cache_row(q, t);
+    float wf[8], cf[8], sf[8];
+    if (hh < q.hq + q.hkv) {
+      const int p = fz::clamp_pos(q, q.positions[t]);
+      fz::unpack8<DT>(*reinterpret_cast<const u32x4*>((hh < q.hq ? q.qw : q.kw) + li * 8), wf);
+      fz::unpack8<DT>(*reinterpret_cast<const u32x4*>(q.cos + (int64_t)p * kHeadDimFused + li * 8), cf);
+      fz::unpack8<DT>(*reinterpret_cast<const u32x4*>(q.sin + (int64_t)p * kHeadDimFused + li * 8), sf);
+    }
+    fz::norm_rope_head<DT>(q, t, hh, li, xr, crow, wf, cf, sf);
+    return;
   }
 
   const int m = m0 + 32 * wm + (lane & 31);
@@ -231,6 +275,16 @@ static int launch_t(Args a, int n_out, hipStream_t st) {
                        dim3(64 * MW * NW * KS), 0, st, a);
     return AAC_OK;
   }
+}
+
+// The QKV projection with the q/k norm + RoPE + store epilogue: 32 tokens x
+// one head per workgroup, K split over two of its 8 waves (the summation
+// order of tiling 8, so q, k and v are those of the plain projection).
+template <bool F16>
+static void launch_qk(Args a, int heads, hipStream_t st) {
+  a.n_tiles = heads;
+  const int grid = (int)cdiv(a.m, 32) * heads;
+  hipLaunchKernelGGL((gemm_kernel<1, 4, 2, 1, false, F16, 3, true>), dim3(grid), dim3(512), 0, st, a);
 }
 
 template <bool SILU, bool F16>
@@ -320,6 +374,80 @@ extern "C" int aac_gemm_nt(const void* x, int64_t x_row_stride, const void* w, i
   else
     rc = silu ? gm::launch_c<true, false>(a, cfg, n, st) : gm::launch_c<false, false>(a, cfg, n, st);
   if (rc != AAC_OK) return rc;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AAC_OK : (int)e;
+}
+
+extern "C" int aac_qkv_norm_rope_store(
+    const void* x, int64_t x_row_stride, const void* w_qkv, int64_t w_row_stride, int64_t n_tokens,
+    int32_t hidden, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+    const void* q_norm_weight, const void* k_norm_weight, float eps, const void* cos_table,
+    const void* sin_table, int32_t max_position, const int32_t* positions, void* q_out, void* k_out,
+    void* k_cache, void* v_cache, int64_t num_cache_rows, const int64_t* slot_mapping,
+    const int32_t* block_tables, int32_t max_blocks_per_seq, const int32_t* cache_seqlens,
+    int32_t block_size, int32_t dtype, void* stream) {
+  if (dtype != AAC_DTYPE_BF16 && dtype != AAC_DTYPE_FP16) return AAC_ERR_UNSUPPORTED;
+  if (head_dim != kHeadDimFused) return AAC_ERR_UNSUPPORTED;
+  if (n_tokens < 0 || hidden <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_position <= 0)
+    return AAC_ERR_INVALID_ARGUMENT;
+  if (hidden % 128) return AAC_ERR_UNSUPPORTED;  // whole 128-column K stages
+  if (x_row_stride < hidden || w_row_stride < hidden) return AAC_ERR_SHAPE;
+  if (n_tokens == 0) return AAC_OK;
+  if (n_tokens >= (int64_t(1) << 31) / 32) return AAC_ERR_UNSUPPORTED;
+  if (!x || !w_qkv || !q_norm_weight || !k_norm_weight || !cos_table || !sin_table || !positions ||
+      !q_out)
+    return AAC_ERR_INVALID_ARGUMENT;
+  if (v_cache) {
+    if (!k_cache) return AAC_ERR_INVALID_ARGUMENT;
+    if (!slot_mapping && (!block_tables || !cache_seqlens || block_size <= 0 || max_blocks_per_seq <= 0))
+      return AAC_ERR_INVALID_ARGUMENT;
+  }
+  if (((uintptr_t)x | (uintptr_t)w_qkv | (uintptr_t)q_out | (uintptr_t)k_out | (uintptr_t)k_cache |
+       (uintptr_t)v_cache | (uintptr_t)cos_table | (uintptr_t)sin_table | (uintptr_t)q_norm_weight |
+       (uintptr_t)k_norm_weight) % 16 ||
+      x_row_stride % 8 || w_row_stride % 8)
+    return AAC_ERR_MISALIGNED;
+  gm::Args a;
+  a.x = (const u16*)x;
+  a.w = (const u16*)w_qkv;
+  a.y = nullptr;
+  a.x_stride = x_row_stride;
+  a.w_stride = w_row_stride;
+  a.y_stride = 0;
+  a.m = (int32_t)n_tokens;
+  a.k = hidden;
+  a.silu_off = 0;
+  a.n_tiles = 0;
+  fz::QkArgs& q = a.qk;
+  q.qkv = nullptr;
+  q.qkv_stride = 0;
+  q.n_tokens = n_tokens;
+  q.hq = n_q_heads;
+  q.hkv = n_kv_heads;
+  q.qw = (const u16*)q_norm_weight;
+  q.kw = (const u16*)k_norm_weight;
+  q.eps = eps;
+  q.cos = (const u16*)cos_table;
+  q.sin = (const u16*)sin_table;
+  q.positions = positions;
+  q.max_pos = max_position;
+  q.q_out = (u16*)q_out;
+  q.k_out = (u16*)k_out;
+  q.k_cache = (u16*)k_cache;
+  q.v_cache = (u16*)v_cache;
+  q.slot_mapping = slot_mapping;
+  q.num_rows = num_cache_rows;
+  q.block_tables = block_tables;
+  q.max_blocks = max_blocks_per_seq;
+  q.cache_seqlens = cache_seqlens;
+  q.block_size = block_size;
+  q.num_blocks = block_size > 0 ? num_cache_rows / block_size : 0;
+  const hipStream_t st = (hipStream_t)stream;
+  const int heads = n_q_heads + 2 * n_kv_heads;
+  if (dtype == AAC_DTYPE_FP16)
+    gm::launch_qk<true>(a, heads, st);
+  else
+    gm::launch_qk<false>(a, heads, st);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? AAC_OK : (int)e;
 }

@@ -9,7 +9,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["rmsnorm", "qk_norm_rope_store", "silu_mul", "linear", "linear_supported"]
+__all__ = ["rmsnorm", "qk_norm_rope_store", "qkv_norm_rope_store", "silu_mul", "linear",
+           "linear_supported"]
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -45,6 +46,28 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     return out if residual is None else (out, res_out)
 
 
+def _cache_args(T, n_kv_heads, k_cache, v_cache, slot_mapping, block_tables, cache_seqlens):
+    """(rows, block_size, table width) of the K/V store arguments, checked."""
+    rows = bs = mb = 0
+    if v_cache is not None:
+        _req(k_cache is not None and k_cache.shape == v_cache.shape and k_cache.is_contiguous()
+             and v_cache.is_contiguous(), "caches must be contiguous and alike")
+        rows = k_cache.numel() // (n_kv_heads * 128)
+        if slot_mapping is None:
+            _req(block_tables is not None and cache_seqlens is not None,
+                 "append needs block_tables and cache_seqlens")
+            _req(block_tables.dtype == torch.int32 and block_tables.is_contiguous()
+                 and block_tables.shape[0] == T, "block_tables must be int32 [T, W]")
+            _req(cache_seqlens.dtype == torch.int32 and cache_seqlens.shape == (T,),
+                 "cache_seqlens must be int32 [T]")
+            bs = k_cache.shape[1]
+            mb = block_tables.shape[1]
+        else:
+            _req(slot_mapping.dtype == torch.int64 and slot_mapping.shape == (T,),
+                 "slot_mapping must be int64 [T]")
+    return rows, bs, mb
+
+
 def qk_norm_rope_store(qkv: torch.Tensor, n_q_heads: int, n_kv_heads: int,
                        q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
                        cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
@@ -65,25 +88,8 @@ def qk_norm_rope_store(qkv: torch.Tensor, n_q_heads: int, n_kv_heads: int,
     _req(positions.dtype == torch.int32 and positions.shape == (T,), "positions must be int32 [T]")
     q = torch.empty((T, n_q_heads, D), dtype=qkv.dtype, device=qkv.device)
     k = torch.empty((T, n_kv_heads, D), dtype=qkv.dtype, device=qkv.device) if want_k else None
-    rows = 0
-    bs = 0
-    mb = 0
-    if v_cache is not None:
-        _req(k_cache is not None and k_cache.shape == v_cache.shape and k_cache.is_contiguous()
-             and v_cache.is_contiguous(), "caches must be contiguous and alike")
-        rows = k_cache.numel() // (n_kv_heads * D)
-        if slot_mapping is None:
-            _req(block_tables is not None and cache_seqlens is not None,
-                 "append needs block_tables and cache_seqlens")
-            _req(block_tables.dtype == torch.int32 and block_tables.is_contiguous()
-                 and block_tables.shape[0] == T, "block_tables must be int32 [T, W]")
-            _req(cache_seqlens.dtype == torch.int32 and cache_seqlens.shape == (T,),
-                 "cache_seqlens must be int32 [T]")
-            bs = k_cache.shape[1]
-            mb = block_tables.shape[1]
-        else:
-            _req(slot_mapping.dtype == torch.int64 and slot_mapping.shape == (T,),
-                 "slot_mapping must be int64 [T]")
+    rows, bs, mb = _cache_args(T, n_kv_heads, k_cache, v_cache, slot_mapping, block_tables,
+                               cache_seqlens)
     rc = _lib.lib().aac_qk_norm_rope_store(
         qkv.data_ptr(), qkv.stride(0), T, n_q_heads, n_kv_heads, D, q_norm_weight.data_ptr(),
         k_norm_weight.data_ptr(), float(eps), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
@@ -95,6 +101,43 @@ def qk_norm_rope_store(qkv: torch.Tensor, n_q_heads: int, n_kv_heads: int,
         cache_seqlens.data_ptr() if (v_cache is not None and slot_mapping is None) else None, bs,
         _code(qkv), _stream(qkv))
     _lib.check(rc, "aac_qk_norm_rope_store")
+    return q, k
+
+
+def qkv_norm_rope_store(x: torch.Tensor, w_qkv: torch.Tensor, n_q_heads: int, n_kv_heads: int,
+                        q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
+                        cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                        k_cache: Optional[torch.Tensor] = None,
+                        v_cache: Optional[torch.Tensor] = None,
+                        slot_mapping: Optional[torch.Tensor] = None,
+                        block_tables: Optional[torch.Tensor] = None,
+                        cache_seqlens: Optional[torch.Tensor] = None, want_k: bool = True):
+    """``qk_norm_rope_store(linear(x, w_qkv), ...)`` in one launch for a decode
+    step's few tokens: the fused QKV projection (model/model.py:132-154), q/k
+    RMSNorm + RoPE (model/model.py:219-228) and the K/V store or append,
+    without the qkv intermediate.  Returns ``(q [T,Hq,128], k [T,Hkv,128] or None)``."""
+    _req(x.is_cuda and x.dim() == 2 and x.stride(1) == 1, "x must be a [T, hidden] GPU tensor")
+    T, hidden = x.shape
+    D = 128
+    _req(w_qkv.dim() == 2 and w_qkv.stride(1) == 1 and w_qkv.dtype == x.dtype
+         and w_qkv.shape == ((n_q_heads + 2 * n_kv_heads) * D, hidden), "w_qkv shape")
+    _req(positions.dtype == torch.int32 and positions.shape == (T,), "positions must be int32 [T]")
+    q = torch.empty((T, n_q_heads, D), dtype=x.dtype, device=x.device)
+    k = torch.empty((T, n_kv_heads, D), dtype=x.dtype, device=x.device) if want_k else None
+    rows, bs, mb = _cache_args(T, n_kv_heads, k_cache, v_cache, slot_mapping, block_tables,
+                               cache_seqlens)
+    rc = _lib.lib().aac_qkv_norm_rope_store(
+        x.data_ptr(), x.stride(0), w_qkv.data_ptr(), w_qkv.stride(0), T, hidden, n_q_heads,
+        n_kv_heads, D, q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), float(eps),
+        cos.data_ptr(), sin.data_ptr(), cos.shape[0], positions.data_ptr(), q.data_ptr(),
+        k.data_ptr() if k is not None else None,
+        k_cache.data_ptr() if v_cache is not None else None,
+        v_cache.data_ptr() if v_cache is not None else None, rows,
+        slot_mapping.data_ptr() if slot_mapping is not None else None,
+        block_tables.data_ptr() if (v_cache is not None and slot_mapping is None) else None, mb,
+        cache_seqlens.data_ptr() if (v_cache is not None and slot_mapping is None) else None, bs,
+        _code(x), _stream(x))
+    _lib.check(rc, "aac_qkv_norm_rope_store")
     return q, k
 
 

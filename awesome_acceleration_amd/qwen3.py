@@ -166,7 +166,7 @@ class Qwen3ForCausalLM:
         self.small_gemm_rows = 512
         self.init_weights(seed)
         H, I = cfg.hidden_size, cfg.intermediate_size
-        if not all(fz.linear_supported(1, n, k) for n, k in (
+        if self.d != 128 or H % 128 or not all(fz.linear_supported(1, n, k) for n, k in (
                 (self.q_size + 2 * self.kv_size, H), (H, self.q_size), (I, H), (H, I))):
             self.small_gemm_rows = 0  # a shape the decode-batch GEMM has no tiling for
         self.rope = Rope(self.d, cfg.max_position_embeddings, cfg.rope_theta, self.device, dtype)
@@ -246,8 +246,9 @@ class Qwen3ForCausalLM:
         RMSNorm, q/k RMSNorm + RoPE + KV store/append, SiLU * up are one launch
         each, and the residual add of each block is folded into the next norm.
         A decode step's projections (one row per sequence) run on the
-        decode-batch GEMM, gate/up with SiLU * up in its epilogue; prefill
-        steps (many rows) keep the library GEMMs."""
+        decode-batch GEMM, QKV with the q/k norm + RoPE + KV append and
+        gate/up with SiLU * up in their epilogues; prefill steps (many rows)
+        keep the library GEMMs."""
         eps = self.cfg.rms_norm_eps
         I = self.cfg.intermediate_size
         h = F.embedding(input_ids, self.embed)
@@ -261,20 +262,28 @@ class Qwen3ForCausalLM:
                 x = fz.rmsnorm(res, L["ln1"], eps)
             else:
                 x, res = fz.rmsnorm(delta, L["ln1"], eps, residual=res)
-            qkv = lin(x, L["qkv"])
-            if prefill:
-                q, k = fz.qk_norm_rope_store(
-                    qkv, self.hq, self.hkv, L["q_norm"], L["k_norm"], eps, self.rope.cos,
-                    self.rope.sin, pos, cache.k(li), cache.v(li), slot_mapping=meta.slot_mapping)
-                v = qkv[:, self.q_size + self.kv_size:].view(T, self.hkv, self.d)
-                attn = fai.flash_attn_varlen_func(q, k, v, meta.cu_seqlens, meta.cu_seqlens,
-                                                  meta.max_seqlen, meta.max_seqlen,
-                                                  softmax_scale=self.scale, causal=True)
-            else:
-                q, _ = fz.qk_norm_rope_store(
-                    qkv, self.hq, self.hkv, L["q_norm"], L["k_norm"], eps, self.rope.cos,
+            if small:  # projection, q/k norm + RoPE and the KV append in one launch
+                q, _ = fz.qkv_norm_rope_store(
+                    x, L["qkv"], self.hq, self.hkv, L["q_norm"], L["k_norm"], eps, self.rope.cos,
                     self.rope.sin, pos, cache.k(li), cache.v(li), block_tables=meta.block_tables,
                     cache_seqlens=meta.cache_seqlens, want_k=False)
+            else:
+                qkv = F.linear(x, L["qkv"])
+                if prefill:
+                    q, k = fz.qk_norm_rope_store(
+                        qkv, self.hq, self.hkv, L["q_norm"], L["k_norm"], eps, self.rope.cos,
+                        self.rope.sin, pos, cache.k(li), cache.v(li), slot_mapping=meta.slot_mapping)
+                    v = qkv[:, self.q_size + self.kv_size:].view(T, self.hkv, self.d)
+                    attn = fai.flash_attn_varlen_func(q, k, v, meta.cu_seqlens, meta.cu_seqlens,
+                                                      meta.max_seqlen, meta.max_seqlen,
+                                                      softmax_scale=self.scale, causal=True)
+                else:
+                    q, _ = fz.qk_norm_rope_store(
+                        qkv, self.hq, self.hkv, L["q_norm"], L["k_norm"], eps, self.rope.cos,
+                        self.rope.sin, pos, cache.k(li), cache.v(li),
+                        block_tables=meta.block_tables, cache_seqlens=meta.cache_seqlens,
+                        want_k=False)
+            if not prefill:
                 attn = fai.decode_paged(q, cache.k(li), cache.v(li), meta.block_tables,
                                         meta.context_lens, softmax_scale=self.scale,
                                         max_context_len=meta.max_context_len)

@@ -267,6 +267,28 @@ int aac_gemm_nt(const void* x, int64_t x_row_stride, const void* w, int64_t w_ro
                 int32_t config, int32_t dtype, void* stream);
 
 /*
+ * The fused QKV projection of a decode step followed by aac_qk_norm_rope_store
+ * in one launch: qkv = x w_qkv^T (x [n_tokens, hidden], w_qkv the fused
+ * [(Hq + 2*Hkv) * 128, hidden] weight, fp32 accumulation rounded to dtype
+ * exactly as aac_gemm_nt's tiling 8 rounds it), then per token the q/k
+ * RMSNorm + RoPE of every q and k head and the K/V store or decode append,
+ * with the arguments and results of aac_qk_norm_rope_store (the [n_tokens,
+ * Hq+2Hkv, 128] qkv intermediate is never written).  hidden must be a
+ * multiple of 128.  Replaces the QKV projection and model/model.py:219-228
+ * plus the k=/v= append of flash_attn_with_kvcache (model/model.py:233-240).
+ */
+int aac_qkv_norm_rope_store(const void* x, int64_t x_row_stride, const void* w_qkv,
+                            int64_t w_row_stride, int64_t n_tokens, int32_t hidden,
+                            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                            const void* q_norm_weight, const void* k_norm_weight, float eps,
+                            const void* cos_table, const void* sin_table, int32_t max_position,
+                            const int32_t* positions, void* q_out, void* k_out, void* k_cache,
+                            void* v_cache, int64_t num_cache_rows, const int64_t* slot_mapping,
+                            const int32_t* block_tables, int32_t max_blocks_per_seq,
+                            const int32_t* cache_seqlens, int32_t block_size, int32_t dtype,
+                            void* stream);
+
+/*
  * KV export: gather the first `length` tokens of one sequence from a paged
  * cache into a contiguous buffer out[n_layers][2][length][Hkv][D] (index 0 =
  * K, 1 = V).  Layer l's K cache starts at kv_cache + l * layer_stride and its

@@ -1,7 +1,8 @@
 """Fused call-site kernels against the reference's own torch expressions:
 RMSNorm (model/model.py:47-52) with the residual add before it, q/k RMSNorm +
 RoPE (model/model.py:86-99, :225-228) with the KV store (llm.py:171-174) or
-decode append, and SiLU * up (model/model.py:188).  The fused kernels round at
+decode append, and SiLU * up (model/model.py:188), and the QKV projection with
+the q/k norm + RoPE + store in its epilogue.  The fused kernels round at
 the same points, so results match to one unit in the last place where fp32
 summation order differs, and the cache stores are bit-exact."""
 import numpy as np
@@ -135,3 +136,47 @@ def test_silu_mul(gpu):
     gu = torch.randn((513, 2 * 3072), generator=g, device=gpu).to(torch.bfloat16)
     ref = F.silu(gu[:, :3072]) * gu[:, 3072:]
     ulp_close(fz.silu_mul(gu), ref, "silu*up")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,hq,hkv,append", [(256, 16, 8, True), (1, 16, 8, True), (37, 16, 8, True),
+                                             (300, 32, 8, True), (100, 16, 8, False)])
+def test_qkv_projection_fused_with_norm_rope_store(gpu, dtype, T, hq, hkv, append):
+    """The QKV projection with q/k norm + RoPE + store in its epilogue equals,
+    bit for bit, the decode-batch GEMM with the same K split (tiling 8)
+    followed by the q/k norm + RoPE + store kernel: q, k and both caches."""
+    print(f"case: qkv projection + norm rope store {dtype} T={T} {hq}/{hkv} append={append}",
+          flush=True)
+    g = torch.Generator(device=gpu).manual_seed(4)
+    D, H, bs = 128, 1024, 16
+    x = torch.randn((T, H), generator=g, device=gpu).to(dtype)
+    w = (torch.randn(((hq + 2 * hkv) * D, H), generator=g, device=gpu) * 0.05).to(dtype)
+    qw = (1 + 0.3 * torch.randn(D, generator=g, device=gpu)).to(dtype)
+    kw = (1 + 0.3 * torch.randn(D, generator=g, device=gpu)).to(dtype)
+    rope = Rope(D, 2048, 1e6, gpu, dtype)
+    W = 8
+    pool = T * W + 1
+    kc = torch.randn((pool, bs, hkv, D), generator=g, device=gpu).to(dtype)
+    vc = torch.randn_like(kc)
+    kc2, vc2 = kc.clone(), vc.clone()
+    if append:
+        bt = (1 + torch.randperm(pool - 1, generator=g, device=gpu)[:T * W]).view(T, W).to(torch.int32)
+        seqlens = torch.randint(0, W * bs, (T,), generator=g, device=gpu, dtype=torch.int32)
+        kwargs = dict(block_tables=bt, cache_seqlens=seqlens)
+        pos = seqlens
+    else:
+        slots = torch.randperm(pool * bs, generator=g, device=gpu)[:T].to(torch.int64)
+        slots[3] = -1  # padding token: not stored
+        kwargs = dict(slot_mapping=slots)
+        pos = torch.randint(0, 2048, (T,), generator=g, device=gpu, dtype=torch.int32)
+    qkv = fz.linear(x, w, config=8)
+    q1, k1 = fz.qk_norm_rope_store(qkv, hq, hkv, qw, kw, 1e-6, rope.cos, rope.sin, pos, kc, vc,
+                                   **kwargs)
+    q2, k2 = fz.qkv_norm_rope_store(x, w, hq, hkv, qw, kw, 1e-6, rope.cos, rope.sin, pos, kc2, vc2,
+                                    **kwargs)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(k1, k2)
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    # and the fused path's q is the reference expression of the projection
+    qn = rms_norm(qkv[:, :hq * D].view(T, hq, D), qw, 1e-6)
+    ulp_close(q2, rope.apply(qn, pos), "q", scale=rope_terms(rope, qn, pos))
