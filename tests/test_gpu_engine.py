@@ -111,3 +111,38 @@ def test_engine_admission_waits_for_blocks(gpu):
     assert llm.allocator.num_free == 4  # every block returned (scratch block excluded)
     with pytest.raises(ValueError):
         llm.generate([[1] * 256])
+
+
+def test_engine_stops_at_eos_with_steps_launched_ahead(gpu):
+    """EOS ends a sequence one step after the step the engine launched ahead
+    of reading it: the tokens must still stop at the first EOS (included, as
+    llm.py:421-425 appends it before stopping), and every sequence must match
+    the synchronous eager loop token for token."""
+    print("case: engine EOS stop with run-ahead decode steps", flush=True)
+    prompts = _prompts(6, 3)
+    _, free_run = _run(False, prompts, [24] * 6)
+    # an EOS id that occurs mid-generation in some sequences but not all
+    counts = {}
+    for o in free_run:
+        for i, t in enumerate(o.token_ids[1:-1], 1):
+            counts.setdefault(t, set()).add(id(o))
+    eos = min((t for t, seqs in counts.items() if 0 < len(seqs) < len(free_run)),
+              key=lambda t: min(o.token_ids.index(t) for o in free_run if t in o.token_ids),
+              default=None)
+    assert eos is not None
+    cfg = Qwen3Config(**{**CFG.__dict__, "eos_token_id": int(eos)})
+    results = {}
+    for graphs in (False, True):
+        llm = LLM(cfg, max_num_seqs=4, max_seq_len=512, block_size=64, seed=0, use_graphs=graphs)
+        futs = [llm.generate([p], max_tokens=24) for p in prompts]
+        results[graphs] = [f.result(timeout=120)[0].token_ids for f in futs]
+        llm.stop()
+    early = 0
+    for toks in results[True]:
+        # stops at the first EOS (kept as the last token) or at max_tokens
+        assert eos not in toks[:-1]
+        assert toks[-1] == eos or len(toks) == 24
+        early += toks[-1] == eos and len(toks) < 24
+    assert early > 0, "no sequence stopped at EOS: the case does not exercise the stop"
+    # graphs with steps launched ahead == the synchronous eager loop
+    assert results[True] == results[False]
