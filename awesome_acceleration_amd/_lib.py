@@ -67,6 +67,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p, _f32, _p, _p, _i32, _p, _p, _p,
          _p, _p, _i64, _p, _p, _i32, _p, _i32, _i32, _p]),
+    "aac_argmax_rows": (_c_int, [_p, _i64, _i64, _i64, _p, _i32, _p]),
     "aac_kv_export_paged": (
         _c_int, [_p, _i64, _i64, _i32, _i64, _i32, _i32, _i32, _p, _i32, _i32, _p, _i32, _p]),
     "aac_kv_import_paged": (

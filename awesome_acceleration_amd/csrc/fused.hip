@@ -15,6 +15,8 @@
 // All three kernels are HBM-bound streaming passes (one read and one write of
 // each tensor).
 
+#include <type_traits>
+
 #include "qk_head.h"
 
 namespace aac {
@@ -157,6 +159,78 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const u16* gu, u16* out, 
   *reinterpret_cast<u32x4*>(out + r * inter + c) = pack8<DT>(o);
 }
 
+// ---------------------------------------------------------------- argmax
+// Greedy sampling (llm.py:215-219, temperature 0): the index of the largest
+// logit of each row, the first one among equal maxima, a NaN counting as
+// larger than every number -- torch.argmax's result.  One workgroup per row;
+// each thread scans 16-byte chunks t, t + 1024, ... (coalesced), keeping
+// its first best, then the workgroup reduces the (value, index) pairs.
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+template <Dt DT>
+__global__ __launch_bounds__(1024) void argmax_kernel(const void* x, int64_t stride, int cols,
+                                                      int64_t* out) {
+  typedef typename std::conditional<DT == Dt::FP32, float, u16>::type T;
+  constexpr int E = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  const int tid = threadIdx.x;
+  const T* p = reinterpret_cast<const T*>(x) + blockIdx.x * stride;
+  auto value = [&](const T* q) {
+    if constexpr (DT == Dt::FP32) return *q;
+    else return Cvt<DT>::lo(*q);
+  };
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  // elements before the row's first 16-byte boundary, whole chunks, the rest
+  const int head = min(cols, (int)(((16 - ((uintptr_t)p & 15)) & 15) / sizeof(T)));
+  const int nch = (cols - head) / E;
+  for (int i = tid; i < head; i += 1024)
+    if (am_better(value(p + i), i, bv, bi)) { bv = value(p + i); bi = i; }
+  for (int c = tid; c < nch; c += 1024) {
+    const int i0 = head + c * E;
+    float v[8];
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p + i0);
+    if constexpr (DT == Dt::FP32) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(w[e]);
+    } else {
+      unpack8<DT>(w, v);
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (am_better(v[e], i0 + e, bv, bi)) { bv = v[e]; bi = i0 + e; }
+  }
+  for (int i = head + nch * E + tid; i < cols; i += 1024)
+    if (am_better(value(p + i), i, bv, bi)) { bv = value(p + i); bi = i; }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  if ((tid & 63) == 0) {
+    sv[tid >> 6] = bv;
+    si[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    bv = tid < 16 ? sv[tid] : -INFINITY;
+    bi = tid < 16 ? si[tid] : 0x7fffffff;
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (tid == 0) out[blockIdx.x] = bi;
+  }
+}
+
 }  // namespace fz
 }  // namespace aac
 
@@ -293,5 +367,26 @@ extern "C" int aac_silu_mul(const void* gate_up, void* out, int64_t n_rows, int3
   else
     hipLaunchKernelGGL((fz::silu_mul_kernel<Dt::FP16>), grid, dim3(256), 0, s,
                        (const u16*)gate_up, (u16*)out, n_rows, intermediate);
+  return fz_status();
+}
+
+extern "C" int aac_argmax_rows(const void* x, int64_t row_stride, int64_t n_rows, int64_t n_cols,
+                               int64_t* out, int32_t dtype, void* stream) {
+  if (dtype != AAC_DTYPE_BF16 && dtype != AAC_DTYPE_FP16 && dtype != AAC_DTYPE_FP32)
+    return AAC_ERR_UNSUPPORTED;
+  if (n_rows < 0 || n_cols <= 0 || row_stride < n_cols) return AAC_ERR_INVALID_ARGUMENT;
+  if (n_cols >= 0x7fffffff || n_rows >= 0x7fffffff) return AAC_ERR_UNSUPPORTED;
+  if (n_rows == 0) return AAC_OK;
+  if (!x || !out) return AAC_ERR_INVALID_ARGUMENT;
+  if ((uintptr_t)x % (dtype == AAC_DTYPE_FP32 ? 4 : 2)) return AAC_ERR_MISALIGNED;
+  const dim3 grid((unsigned)n_rows);
+  hipStream_t s = (hipStream_t)stream;
+  const int cols = (int)n_cols;
+  if (dtype == AAC_DTYPE_BF16)
+    hipLaunchKernelGGL((fz::argmax_kernel<Dt::BF16>), grid, dim3(1024), 0, s, x, row_stride, cols, out);
+  else if (dtype == AAC_DTYPE_FP16)
+    hipLaunchKernelGGL((fz::argmax_kernel<Dt::FP16>), grid, dim3(1024), 0, s, x, row_stride, cols, out);
+  else
+    hipLaunchKernelGGL((fz::argmax_kernel<Dt::FP32>), grid, dim3(1024), 0, s, x, row_stride, cols, out);
   return fz_status();
 }

@@ -10,7 +10,7 @@ import torch
 from . import _lib
 
 __all__ = ["rmsnorm", "qk_norm_rope_store", "qkv_norm_rope_store", "silu_mul", "linear",
-           "linear_supported"]
+           "linear_supported", "argmax"]
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -174,4 +174,17 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     rc = _lib.lib().aac_silu_mul(gate_up.data_ptr(), out.data_ptr(), rows, two_i // 2,
                                  _code(gate_up), _stream(gate_up))
     _lib.check(rc, "aac_silu_mul")
+    return out
+
+
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    """``logits.argmax(dim=-1)`` of a [rows, cols] GPU tensor (int64), the
+    greedy sampler of llm.py:215-219: the first index of each row's maximum."""
+    _req(logits.is_cuda and logits.dim() == 2 and logits.stride(1) == 1, "logits must be [rows, cols]")
+    _req(logits.dtype in _lib.AAC_DTYPE, f"unsupported dtype {logits.dtype}")
+    out = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
+    rc = _lib.lib().aac_argmax_rows(logits.data_ptr(), logits.stride(0), logits.shape[0],
+                                    logits.shape[1], out.data_ptr(), _lib.AAC_DTYPE[logits.dtype],
+                                    _stream(logits))
+    _lib.check(rc, "aac_argmax_rows")
     return out

@@ -42,6 +42,7 @@ from typing import Callable, Optional
 import numpy as np
 import torch
 
+from . import fused as fz
 from .paged import BlockAllocator, build_prefill_metadata, pad_block_tables
 from .qwen3 import PagedKVCache, Qwen3Config, Qwen3ForCausalLM, StepMeta
 
@@ -164,7 +165,7 @@ class LLM:
     # ------------------------------------------------------------ core steps
     def _sample(self, logits: torch.Tensor, temperature: float) -> list[int]:
         if temperature == 0:
-            return logits.argmax(dim=-1).tolist()
+            return fz.argmax(logits).tolist()
         probs = torch.softmax(logits.float() / temperature, dim=-1)
         return torch.multinomial(probs, 1).squeeze(-1).tolist()
 
@@ -234,7 +235,7 @@ class LLM:
         B, W = self._bucket(n), self.blocks_per_seq
         logits = self._graphs[B][1]
         if temperature == 0:
-            tok = logits.argmax(dim=-1)
+            tok = fz.argmax(logits)
         else:
             tok = torch.multinomial(torch.softmax(logits.float() / temperature, dim=-1), 1)
             tok = tok.squeeze(-1)

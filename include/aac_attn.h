@@ -289,6 +289,16 @@ int aac_qkv_norm_rope_store(const void* x, int64_t x_row_stride, const void* w_q
                             void* stream);
 
 /*
+ * Greedy sampling: out[r] = the index of the largest element of row r of x
+ * [n_rows, n_cols] (row stride row_stride elements; BF16, FP16 or FP32), the
+ * first one among equal maxima, a NaN counting as the largest -- the result
+ * of torch.argmax(dim=-1).  Replaces logits.argmax(dim=-1) of the sampler
+ * (llm.py:215-219, temperature 0).
+ */
+int aac_argmax_rows(const void* x, int64_t row_stride, int64_t n_rows, int64_t n_cols,
+                    int64_t* out, int32_t dtype, void* stream);
+
+/*
  * KV export: gather the first `length` tokens of one sequence from a paged
  * cache into a contiguous buffer out[n_layers][2][length][Hkv][D] (index 0 =
  * K, 1 = V).  Layer l's K cache starts at kv_cache + l * layer_stride and its

@@ -180,3 +180,27 @@ def test_qkv_projection_fused_with_norm_rope_store(gpu, dtype, T, hq, hkv, appen
     # and the fused path's q is the reference expression of the projection
     qn = rms_norm(qkv[:, :hq * D].view(T, hq, D), qw, 1e-6)
     ulp_close(q2, rope.apply(qn, pos), "q", scale=rope_terms(rope, qn, pos))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,cols,pad", [(256, 151936, 0), (7, 1001, 24), (1, 5, 3), (3, 2048, 0)])
+def test_argmax_matches_torch(gpu, dtype, rows, cols, pad):
+    """Row argmax (the greedy sampler) equals torch.argmax(dim=-1): random
+    rows, rows with repeated maxima (first index wins), all -inf rows, NaNs
+    (a NaN counts as the maximum), strided rows, odd widths."""
+    print(f"case: argmax {dtype} {rows}x{cols} pad {pad}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(6)
+    base = torch.randn((rows, cols + pad), generator=g, device=gpu).to(dtype)
+    x = base[:, :cols]
+    if rows >= 3 and cols >= 5:
+        x[0, :] = x[0, 0]                   # all equal: index 0
+        x[1, :] = -float("inf")             # all -inf: index 0
+        x[2, cols // 3] = float("nan")      # NaN wins
+        x[2, cols - 1] = float("nan")       # ... the first NaN
+    if rows >= 5:
+        m = x[4].max()
+        x[4, cols - 1] = m                  # a tie with an earlier maximum
+    got = fz.argmax(x)
+    ref = torch.argmax(x, dim=-1)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref), (got[:8].tolist(), ref[:8].tolist())
