@@ -356,7 +356,7 @@ extern "C" int aac_gemm_nt(const void* x, int64_t x_row_stride, const void* w, i
   const int tc = 32 * gm::kCfg[cfg][1];
   if (n % tc || k % gm::kCfg[cfg][2]) return AAC_ERR_UNSUPPORTED;
   if (cdiv(m, 32 * gm::kCfg[cfg][0]) * (n / tc) >= (int64_t(1) << 31)) return AAC_ERR_UNSUPPORTED;
-  gm::Args a;
+  gm::Args a{};
   a.x = (const u16*)x;
   a.w = (const u16*)w;
   a.y = (u16*)y;
@@ -407,7 +407,7 @@ extern "C" int aac_qkv_norm_rope_store(
        (uintptr_t)k_norm_weight) % 16 ||
       x_row_stride % 8 || w_row_stride % 8)
     return AAC_ERR_MISALIGNED;
-  gm::Args a;
+  gm::Args a{};
   a.x = (const u16*)x;
   a.w = (const u16*)w_qkv;
   a.y = nullptr;
