@@ -257,7 +257,8 @@ int aac_silu_mul(const void* gate_up, void* out, int64_t n_rows, int32_t interme
  * (model/model.py:188) -- the product of aac_silu_mul without the [m, 2I]
  * intermediate.  Built for shapes where n is a multiple of 32 and k of 64
  * (of 128 / 256 for some tilings); config 0 lets the library pick the tiling,
- * 1..4 force one (tuning).  Meant for the small m of a decode step (tens to
+ * 1..6 force one (tuning; a tiling whose stages do not fit LDS with the
+ * gate/up pairing returns AAC_ERR_UNSUPPORTED).  Meant for the small m of a decode step (tens to
  * hundreds of rows): every output tile is one workgroup.
  * Replaces the q/k/v, o_proj, gate/up and down nn.Linear calls of the
  * decoder layer (model/model.py:132-154, :258, :178-188) on decode steps.
@@ -270,7 +271,7 @@ int aac_gemm_nt(const void* x, int64_t x_row_stride, const void* w, int64_t w_ro
  * The fused QKV projection of a decode step followed by aac_qk_norm_rope_store
  * in one launch: qkv = x w_qkv^T (x [n_tokens, hidden], w_qkv the fused
  * [(Hq + 2*Hkv) * 128, hidden] weight, fp32 accumulation rounded to dtype
- * exactly as aac_gemm_nt's tiling 8 rounds it), then per token the q/k
+ * exactly as aac_gemm_nt's tiling 6 rounds it), then per token the q/k
  * RMSNorm + RoPE of every q and k head and the K/V store or decode append,
  * with the arguments and results of aac_qk_norm_rope_store (the [n_tokens,
  * Hq+2Hkv, 128] qkv intermediate is never written).  hidden must be a

@@ -143,7 +143,7 @@ def test_silu_mul(gpu):
                                              (300, 32, 8, True), (100, 16, 8, False)])
 def test_qkv_projection_fused_with_norm_rope_store(gpu, dtype, T, hq, hkv, append):
     """The QKV projection with q/k norm + RoPE + store in its epilogue equals,
-    bit for bit, the decode-batch GEMM with the same K split (tiling 8)
+    bit for bit, the decode-batch GEMM with the same K split (tiling 6)
     followed by the q/k norm + RoPE + store kernel: q, k and both caches."""
     print(f"case: qkv projection + norm rope store {dtype} T={T} {hq}/{hkv} append={append}",
           flush=True)
@@ -169,7 +169,7 @@ def test_qkv_projection_fused_with_norm_rope_store(gpu, dtype, T, hq, hkv, appen
         slots[3] = -1  # padding token: not stored
         kwargs = dict(slot_mapping=slots)
         pos = torch.randint(0, 2048, (T,), generator=g, device=gpu, dtype=torch.int32)
-    qkv = fz.linear(x, w, config=8)
+    qkv = fz.linear(x, w, config=6)
     q1, k1 = fz.qk_norm_rope_store(qkv, hq, hkv, qw, kw, 1e-6, rope.cos, rope.sin, pos, kc, vc,
                                    **kwargs)
     q2, k2 = fz.qkv_norm_rope_store(x, w, hq, hkv, qw, kw, 1e-6, rope.cos, rope.sin, pos, kc2, vc2,

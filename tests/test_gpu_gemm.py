@@ -53,7 +53,7 @@ def test_linear_matches_fp32_reference(gpu, m, n, k, dtype):
     _check_linear(y, x, w, f"{m}x{n}x{k} {dtype}")
 
 
-@pytest.mark.parametrize("config", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5, 6])
 def test_every_tiling(gpu, config):
     """Each forced tiling on a shape all of them support, with strided rows."""
     m, n, k = 200, 512, 1024
@@ -76,7 +76,7 @@ def _silu_ref(x, w):
 @pytest.mark.parametrize("m,i,k,config", [
     (256, 3072, 1024, 0),  # gate/up of a Qwen3-0.6B decode step
     (256, 3072, 1024, 1), (256, 3072, 1024, 2), (256, 3072, 1024, 4),
-    (200, 3072, 1024, 3), (37, 3072, 1024, 0), (256, 3072, 1024, 7), (100, 3072, 1024, 8),
+    (200, 3072, 1024, 3), (37, 3072, 1024, 0), (100, 3072, 1024, 6),
     (5, 3072, 1024, 0), (130, 256, 512, 0),
 ])
 def test_silu_gate_up_matches_reference(gpu, m, i, k, config, dtype):
@@ -99,6 +99,15 @@ def test_silu_gate_up_matches_reference(gpu, m, i, k, config, dtype):
     # and most elements are identical (the products round the same way)
     frac = float((err > 0).float().mean())
     assert frac < 0.05, f"{frac:.2%} of the elements differ"
+
+
+def test_gate_up_tiling_that_does_not_fit_lds_is_rejected(gpu):
+    """Tiling 5 stages 128 rows x 256 K with the gate/up pairing: three stages
+    exceed LDS, so the call fails with an error instead of launching."""
+    x = torch.zeros((64, 1024), device=gpu, dtype=torch.bfloat16)
+    w = torch.zeros((2 * 3072, 1024), device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        fz.linear(x, w, silu=True, config=5)
 
 
 def test_rejects_bad_arguments(gpu):
