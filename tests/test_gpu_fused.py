@@ -140,7 +140,8 @@ def test_silu_mul(gpu):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T,hq,hkv,append", [(256, 16, 8, True), (1, 16, 8, True), (37, 16, 8, True),
-                                             (300, 32, 8, True), (100, 16, 8, False)])
+                                             (300, 32, 8, True), (100, 16, 8, False),
+                                             (512, 16, 8, True)])
 def test_qkv_projection_fused_with_norm_rope_store(gpu, dtype, T, hq, hkv, append):
     """The QKV projection with q/k norm + RoPE + store in its epilogue equals,
     bit for bit, the decode-batch GEMM with the same K split (tiling 6)

@@ -45,6 +45,7 @@ def _check_linear(y, x, w, what):
     (256, 1024, 2048),   # o_proj
     (256, 1024, 3072),   # down
     (1, 4096, 1024), (7, 1024, 2048), (100, 4096, 1024), (300, 1024, 3072), (64, 192, 256),
+    (512, 4096, 1024), (512, 1024, 3072),  # the largest decode batch the model sends here
 ])
 def test_linear_matches_fp32_reference(gpu, m, n, k, dtype):
     x, w = _inputs(gpu, m, n, k, dtype, seed=m + n + k)
@@ -77,7 +78,7 @@ def _silu_ref(x, w):
     (256, 3072, 1024, 0),  # gate/up of a Qwen3-0.6B decode step
     (256, 3072, 1024, 1), (256, 3072, 1024, 2), (256, 3072, 1024, 4),
     (200, 3072, 1024, 3), (37, 3072, 1024, 0), (100, 3072, 1024, 6),
-    (5, 3072, 1024, 0), (130, 256, 512, 0),
+    (5, 3072, 1024, 0), (130, 256, 512, 0), (512, 3072, 1024, 0),
 ])
 def test_silu_gate_up_matches_reference(gpu, m, i, k, config, dtype):
     x, w = _inputs(gpu, m, 2 * i, k, dtype, seed=7 * m + i)
