@@ -106,6 +106,26 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------- KV store
+def check_mode() -> bool:
+    """Whether ``AAC_CHECK`` is set: the stores then validate slot_mapping as
+    ``index_copy_`` does (one device sync per call)."""
+    return _CHECK
+
+
+def _check_slots(slot_mapping: torch.Tensor, rows: int) -> None:
+    """With ``AAC_CHECK``: ``IndexError`` for any slot outside ``[0, rows)``,
+    negative ones included -- the contract of the reference's ``index_copy_``
+    (llm.py:171-174).  Without it the kernels skip such slots (a negative slot
+    is the padding convention of paged engines), and the engine validates its
+    own slot mappings on the host (``paged.check_slots``)."""
+    if _CHECK and slot_mapping.numel():
+        lo, hi = torch.aminmax(slot_mapping)
+        lo, hi = int(lo), int(hi)
+        if lo < 0 or hi >= rows:
+            bad = lo if lo < 0 else hi
+            raise IndexError(f"index {bad} is out of bounds for dimension 0 with size {rows}")
+
+
 def kv_store(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
              slot_mapping: torch.Tensor) -> None:
     """``k_cache.view(-1,Hkv,D).index_copy_(0, slot_mapping, k)`` and the same for v.
@@ -113,8 +133,9 @@ def kv_store(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: t
     Replaces llm.py:171-174.  ``k``/``v`` are ``[N, Hkv, D]`` (any token
     stride, e.g. v as a view of the fused qkv buffer); the caches are
     contiguous ``[..., Hkv, D]``; ``slot_mapping`` is int64 ``[N]`` on the
-    device.  Negative slots are skipped.  With ``AAC_CHECK=1`` out-of-range
-    slots raise ``IndexError`` like ``index_copy_`` (this synchronises).
+    device.  Negative and out-of-range slots are skipped.  With ``AAC_CHECK=1``
+    any slot outside ``[0, rows)`` raises ``IndexError`` like ``index_copy_``
+    (this synchronises).
     """
     _on_gpu(k, v, k_cache, v_cache, slot_mapping)
     ks, vs = _token_rows(k, "k"), _token_rows(v, "v")
@@ -127,9 +148,7 @@ def kv_store(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: t
              and slot_mapping.shape[0] == k.shape[0], "slot_mapping must be int64 [N]")
     _require(slot_mapping.is_contiguous(), "slot_mapping must be contiguous")
     rows = k_cache.numel() // (k.shape[1] * k.shape[2])
-    if _CHECK and slot_mapping.numel():
-        if int(slot_mapping.max()) >= rows:
-            raise IndexError("slot_mapping entry out of range")
+    _check_slots(slot_mapping, rows)
     rc = _lib.lib().aac_kv_store(
         k.data_ptr(), v.data_ptr(), ks, vs, k_cache.data_ptr(), v_cache.data_ptr(), rows,
         slot_mapping.data_ptr(), k.shape[0], k.shape[1], k.shape[2], _dtype_code(k), _stream(k))
@@ -208,9 +227,7 @@ def varlen_prefill_with_kvcache(q, k, v, cu_seqlens, max_seqlen, k_cache, v_cach
              and slot_mapping.shape[0] == k.shape[0] and slot_mapping.is_contiguous(),
              "slot_mapping must be contiguous int64 [N]")
     rows = k_cache.numel() // (k.shape[1] * k.shape[2])
-    if _CHECK and slot_mapping.numel():
-        if int(slot_mapping.max()) >= rows:
-            raise IndexError("slot_mapping entry out of range")
+    _check_slots(slot_mapping, rows)
     scale = q.shape[-1] ** -0.5 if softmax_scale is None else float(softmax_scale)
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     rc = _lib.lib().aac_prefill_varlen_store(

@@ -10,7 +10,7 @@ import torch
 from . import _lib
 
 __all__ = ["rmsnorm", "qk_norm_rope_store", "qkv_norm_rope_store", "silu_mul", "linear",
-           "linear_supported", "argmax"]
+           "linear_supported", "rmsnorm_supported", "argmax"]
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -162,8 +162,16 @@ def linear(x: torch.Tensor, weight: torch.Tensor, silu: bool = False,
 
 
 def linear_supported(m: int, n: int, k: int) -> bool:
-    """Whether aac_gemm_nt has a tiling for this shape."""
-    return m > 0 and ((n % 64 == 0 and k % 64 == 0) or (n % 32 == 0 and k % 128 == 0))
+    """Whether aac_gemm_nt's own tiling choice (config 0) has a tiling for this
+    shape: every tiling it picks from needs n % 32 == 0 and k % 128 == 0
+    (whole 32-column output tiles, whole 128-element K stages)."""
+    return m > 0 and n % 32 == 0 and k % 128 == 0
+
+
+def rmsnorm_supported(hidden: int) -> bool:
+    """Whether aac_rmsnorm handles rows of ``hidden`` elements (one wavefront
+    per row, 8 elements per lane per pass: a multiple of 512, at most 4096)."""
+    return hidden > 0 and hidden % 512 == 0 and hidden <= 4096
 
 
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:

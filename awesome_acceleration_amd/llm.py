@@ -133,12 +133,19 @@ class LLM:
         in prompt order (llm.py:225-264)."""
         if not prompts:
             raise ValueError("no prompts")
+        pool = self.allocator.num_blocks - 1  # block 0 is the scratch block
         for p in prompts:
             if not p:
                 raise ValueError("empty prompt")
             if len(p) >= self.max_seq_len:
                 raise ValueError(f"prompt of {len(p)} tokens does not fit max_seq_len "
                                  f"{self.max_seq_len}")
+            if self._blocks_for(len(p), max_tokens) > pool:
+                # admission reserves every block a sequence can reach up front;
+                # a request that needs more than the whole pool would wait forever
+                raise ValueError(f"prompt of {len(p)} tokens with max_tokens {max_tokens} needs "
+                                 f"{self._blocks_for(len(p), max_tokens)} KV blocks; the pool "
+                                 f"has {pool}")
         self._ensure_loop()
         fut: concurrent.futures.Future = concurrent.futures.Future()
         req = _Request(token_ids=[list(map(int, p)) for p in prompts], max_tokens=max_tokens,
@@ -146,6 +153,10 @@ class LLM:
                        results=[None] * len(prompts), pending_indices=list(range(len(prompts))))
         self._request_queue.put(req)
         return fut
+
+    def _blocks_for(self, prompt_len: int, max_tokens: int) -> int:
+        """KV blocks reserved at admission: every position the sequence can reach."""
+        return math.ceil(min(prompt_len + max_tokens, self.max_seq_len) / self.block_size)
 
     def stop(self, timeout: float = 30.0):
         """Stop the background loop (llm.py:302-309)."""
@@ -174,7 +185,11 @@ class LLM:
         prompts = [s.req.token_ids[s.prompt_idx] for s in seqs]
         lens = [len(p) for p in prompts]
         tables = pad_block_tables([s.blocks for s in seqs], self.blocks_per_seq)
-        cu, positions, slots = build_prefill_metadata(lens, tables, self.block_size, self.device)
+        # a slot outside the cache raises IndexError here, before any launch,
+        # as the reference's index_copy_ store does (llm.py:171-174)
+        cu, positions, slots = build_prefill_metadata(
+            lens, tables, self.block_size, self.device,
+            num_cache_rows=self.cache.num_blocks * self.block_size)
         ids = torch.from_numpy(np.fromiter((t for p in prompts for t in p), dtype=np.int64,
                                            count=sum(lens))).to(self.device)
         last = (cu[1:] - 1).long()
@@ -209,6 +224,13 @@ class LLM:
         tab = h[4 * B:4 * B + B * W].reshape(B, W)
         for i, s in enumerate(seqs):
             tab[i, :len(s.blocks)] = s.blocks
+        # every sequence's append row must be a row of its own blocks (the
+        # error the reference's store raises for a bad index, llm.py:171-174);
+        # padding rows append into the scratch block 0
+        if (int(tab[:n].max(initial=0)) >= self.cache.num_blocks or int(tab[:n].min(initial=0)) < 0
+                or any(s.pos >= len(s.blocks) * self.block_size for s in seqs)):
+            raise IndexError(f"decode append outside the KV cache ({self.cache.num_blocks} blocks "
+                             f"of {self.block_size})")
         h[4 * B + B * W:4 * B + B * W + n] = 1        # live rows
         m = B * (5 + W)
         self._dev[:m].copy_(self._host[:m], non_blocking=True)
@@ -335,7 +357,7 @@ class LLM:
                     while req.pending_indices and free_rows:
                         pi = req.pending_indices[0]
                         L = len(req.token_ids[pi])
-                        need = math.ceil(min(L + req.max_tokens, self.max_seq_len) / self.block_size)
+                        need = self._blocks_for(L, req.max_tokens)
                         if need > self.allocator.num_free:
                             break
                         req.pending_indices.pop(0)

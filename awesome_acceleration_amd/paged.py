@@ -31,6 +31,8 @@ __all__ = [
     "decode_slot_mapping",
     "build_prefill_metadata",
     "pad_block_tables",
+    "check_slots",
+    "padded_prefill_slot_mapping",
 ]
 
 
@@ -121,39 +123,92 @@ def pad_block_tables(tables: Sequence[Sequence[int]], width: int | None = None,
     return out
 
 
+def check_slots(slots: np.ndarray, num_cache_rows: int) -> None:
+    """Raise ``IndexError`` unless every slot is a row of the cache, as the
+    reference's ``index_copy_`` into ``[num_cache_rows, Hkv, D]`` rejects an
+    index outside ``[0, num_cache_rows)`` (llm.py:171-174).  Host-side: the
+    engine builds its slot mappings here, so the check costs no device sync."""
+    s = np.asarray(slots)
+    if s.size and (int(s.min()) < 0 or int(s.max()) >= num_cache_rows):
+        bad = int(s.min()) if int(s.min()) < 0 else int(s.max())
+        raise IndexError(f"index {bad} is out of bounds for dimension 0 with size {num_cache_rows}")
+
+
+def _table_rows(bt: np.ndarray, rows: np.ndarray, p: np.ndarray, block_size: int) -> np.ndarray:
+    """Cache rows of positions ``p`` of sequences ``rows`` through the tables;
+    a position past a table's width raises ``IndexError``."""
+    blk = p // block_size
+    if blk.size and (int(blk.min()) < 0 or int(blk.max()) >= bt.shape[1]):
+        raise IndexError(f"position {int(p.max())} is past the block table "
+                         f"({bt.shape[1]} blocks of {block_size})")
+    return bt[rows, blk] * block_size + p % block_size
+
+
 def prefill_slot_mapping(block_tables: np.ndarray, seq_lens: Sequence[int], block_size: int,
-                         start_positions: Sequence[int] | None = None) -> np.ndarray:
-    """Flat cache row of every packed prefill token (paged form of llm.py:139-140)."""
+                         start_positions: Sequence[int] | None = None,
+                         num_cache_rows: int | None = None) -> np.ndarray:
+    """Flat cache row of every packed prefill token (paged form of llm.py:139-140).
+
+    With ``num_cache_rows`` every row is checked against the cache
+    (``IndexError`` as ``index_copy_`` raises)."""
     bt = np.asarray(block_tables, dtype=np.int64)
     parts = []
     for b, L in enumerate(seq_lens):
         p0 = 0 if start_positions is None else int(start_positions[b])
         p = np.arange(p0, p0 + int(L), dtype=np.int64)
-        parts.append(bt[b, p // block_size] * block_size + p % block_size)
-    return np.concatenate(parts) if parts else np.zeros(0, dtype=np.int64)
+        parts.append(_table_rows(bt, np.full(p.shape, b), p, block_size))
+    out = np.concatenate(parts) if parts else np.zeros(0, dtype=np.int64)
+    if num_cache_rows is not None:
+        check_slots(out, num_cache_rows)
+    return out
 
 
 def decode_slot_mapping(block_tables: np.ndarray, positions: Sequence[int],
-                        block_size: int) -> np.ndarray:
-    """Flat cache row of the token each decode sequence appends at ``positions[b]``."""
+                        block_size: int, num_cache_rows: int | None = None) -> np.ndarray:
+    """Flat cache row of the token each decode sequence appends at ``positions[b]``
+    (checked against the cache with ``num_cache_rows``, as above)."""
     bt = np.asarray(block_tables, dtype=np.int64)
     p = np.asarray(positions, dtype=np.int64)
-    return bt[np.arange(p.shape[0]), p // block_size] * block_size + p % block_size
+    out = _table_rows(bt, np.arange(p.shape[0]), p, block_size)
+    if num_cache_rows is not None:
+        check_slots(out, num_cache_rows)
+    return out
+
+
+def padded_prefill_slot_mapping(slot_indices: Sequence[int], seq_lens: Sequence[int],
+                                padded_len: int, max_seq_len: int) -> np.ndarray:
+    """Slot mapping that turns the padded prefill branch's per-slot stores
+    ``k_cache[slot_i, :L_i] = k[i, :L_i]`` (model/model.py:244-250, over
+    ``k [B, T, Hkv, D]`` flattened to ``[B*T, Hkv, D]``) into one ``kv_store``
+    call: token ``t`` of row ``i`` goes to cache row ``slot_i * max_seq_len + t``
+    for ``t < L_i``; padding tokens get -1, which the store skips."""
+    B, T = len(slot_indices), int(padded_len)
+    if len(seq_lens) != B:
+        raise ValueError("one sequence length per slot")
+    out = np.full((B, T), -1, dtype=np.int64)
+    t = np.arange(T, dtype=np.int64)
+    for i, (slot, L) in enumerate(zip(slot_indices, seq_lens)):
+        if not 0 <= int(L) <= min(T, max_seq_len):
+            raise ValueError(f"sequence length {L} outside [0, min(padded_len, max_seq_len)]")
+        out[i, :L] = int(slot) * max_seq_len + t[:L]
+    return out.reshape(-1)
 
 
 def build_prefill_metadata(seq_lens: Sequence[int], block_tables: np.ndarray, block_size: int,
-                           device: torch.device | str):
+                           device: torch.device | str, num_cache_rows: int | None = None):
     """``(cu_seqlens int32 [n+1], positions int64 [N], slot_mapping int64 [N])`` on ``device``.
 
     Same values as llm.py:129-140 for the slot layout; each tensor is built on
     the host and copied once (the reference issues one small copy per list
-    and a device-side ``repeat_interleave``).
+    and a device-side ``repeat_interleave``).  With ``num_cache_rows`` a slot
+    outside the cache raises ``IndexError`` before anything is copied, the
+    error the reference's ``index_copy_`` store raises (llm.py:171-174).
     """
     lens = np.asarray(seq_lens, dtype=np.int64)
     cu = np.zeros(lens.shape[0] + 1, dtype=np.int32)
     np.cumsum(lens, out=cu[1:])
     positions = (np.concatenate([np.arange(L, dtype=np.int64) for L in lens])
                  if lens.size else np.zeros(0, dtype=np.int64))
-    slots = prefill_slot_mapping(block_tables, lens, block_size)
+    slots = prefill_slot_mapping(block_tables, lens, block_size, num_cache_rows=num_cache_rows)
     to = lambda a: torch.from_numpy(a).to(device, non_blocking=False)  # noqa: E731
     return to(cu), to(positions), to(slots)

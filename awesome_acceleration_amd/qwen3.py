@@ -154,7 +154,10 @@ class Qwen3ForCausalLM:
     def __init__(self, cfg: Qwen3Config, device, dtype=torch.bfloat16, seed: int = 0,
                  fused: bool = True):
         self.cfg = cfg
-        self.fused = fused
+        # the fused call-site kernels need head_dim 128 and a hidden size the
+        # RMSNorm kernel covers; other shapes run the unfused torch layer
+        self.fused = (fused and cfg.head_dim == 128
+                      and fz.rmsnorm_supported(cfg.hidden_size))
         self.device = torch.device(device)
         self.dtype = dtype
         self.hq, self.hkv, self.d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim

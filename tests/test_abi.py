@@ -21,6 +21,54 @@ def test_header_and_binding_agree():
     assert declared_functions() == sorted(_lib.SIGNATURES)
 
 
+def declared_prototypes():
+    """name -> (return type, [parameter types]) parsed from the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"([\w\s\*]+?)\b(aac_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(3).split(",") if p.strip() and p.strip() != "void"]
+        # drop the parameter name: the type is everything before the last identifier
+        types = [re.sub(r"\b\w+$", "", p).strip() for p in params]
+        out[m.group(2)] = (m.group(1).split()[-1] if m.group(1).split() else "", types)
+    return out
+
+
+def _type_class(c_type: str) -> str:
+    t = c_type.replace("const", "").strip()
+    if "*" in t:
+        return "char*" if t.replace(" ", "") == "char*" else "pointer"
+    return {"int": "int32", "int32_t": "int32", "int64_t": "int64", "float": "float",
+            "size_t": "size_t"}[t]
+
+
+def _ctypes_class(ct) -> str:
+    if ct in (ctypes.c_void_p,):
+        return "pointer"
+    if ct is ctypes.c_char_p:
+        return "char*"
+    if ct is ctypes.c_float:
+        return "float"
+    if ct is ctypes.c_size_t:
+        return "size_t"
+    return {4: "int32", 8: "int64"}[ctypes.sizeof(ct)]
+
+
+def test_binding_parameter_types_match_the_header():
+    """Every argtype of the ctypes binding has the width and kind of the
+    header's parameter at that position (a drift would corrupt arguments)."""
+    protos = declared_prototypes()
+    assert sorted(protos) == sorted(_lib.SIGNATURES)
+    for name, (res, args) in _lib.SIGNATURES.items():
+        ret, params = protos[name]
+        assert len(params) == len(args), (name, len(params), len(args))
+        for i, (cp, ct) in enumerate(zip(params, args)):
+            assert _type_class(cp) == _ctypes_class(ct), (name, i, cp, ct)
+        if ret == "char*" or name == "aac_strerror":
+            assert res is ctypes.c_char_p
+        else:
+            assert _type_class(ret) == _ctypes_class(res), (name, ret, res)
+
+
 def test_library_exports_every_declared_symbol():
     assert LIB_PATH.exists(), "build the library first (__graft_entry__.build())"
     handle = ctypes.CDLL(str(LIB_PATH))

@@ -146,3 +146,98 @@ def test_engine_stops_at_eos_with_steps_launched_ahead(gpu):
     assert early > 0, "no sequence stopped at EOS: the case does not exercise the stop"
     # graphs with steps launched ahead == the synchronous eager loop
     assert results[True] == results[False]
+
+
+def test_engine_raises_index_error_for_a_slot_outside_the_cache(gpu):
+    """The engine's store path keeps the reference's index_copy_ contract
+    (llm.py:171-174): a block id outside the cache raises IndexError on the
+    host before any launch, for a prefill and for a decode step."""
+    print("case: engine IndexError for an out-of-range slot", flush=True)
+    from awesome_acceleration_amd.llm import _Request, _Seq
+    import concurrent.futures
+    llm = LLM(CFG, max_num_seqs=2, max_seq_len=256, block_size=64, num_blocks=3, seed=0,
+              use_graphs=False)
+    req = _Request(token_ids=[[3] * 70], max_tokens=4, temperature=0.0, ignore_eos=True,
+                   future=concurrent.futures.Future())
+    bad = _Seq(req, 0, 0, [1, llm.cache.num_blocks + 3], [], 70)
+    before = llm.cache.storage.clone()
+    with pytest.raises(IndexError):
+        llm._prefill([bad])
+    bad.tokens.append(5)
+    bad.pos = 70  # appends into the second (bad) block
+    with pytest.raises(IndexError):
+        llm._decode_step([bad])
+    short = _Seq(req, 0, 0, [1], [5], 64)  # position 64 is past its one block
+    with pytest.raises(IndexError):
+        llm._decode_step([short])
+    torch.cuda.synchronize()
+    assert torch.equal(llm.cache.storage, before)
+    # a request larger than the whole pool is refused at submission and the
+    # loop stays serviceable (no busy wait on an unadmittable request)
+    with pytest.raises(ValueError, match="KV blocks"):
+        llm.generate([[1] * 200], max_tokens=400)
+    out = llm.generate([[1] * 50], max_tokens=5, ignore_eos=True).result(timeout=60)
+    assert out[0].generated_tokens == 5
+    llm.stop(timeout=10)
+    assert llm._loop_thread is None
+
+
+REAL = Qwen3Config()  # Qwen3-0.6B: 28 layers, hidden 1024, 16/8 heads, vocab 151936
+
+
+def test_qwen3_0p6b_engine_tokens_match_fp32_reference(gpu):
+    """The engine at the real Qwen3-0.6B shape (28 layers, hidden 1024, 16/8
+    heads, vocab 151,936, KV block 256, the 256-row decode batch of the
+    256 x 1024/1024 workload): a few ~1000-token prompts with 32 greedy
+    tokens each, teacher-forced against the fp32 forward of the same
+    weights (margin-gated, as above)."""
+    print("case: Qwen3-0.6B engine vs fp32 reference (4 requests x ~1000/32)", flush=True)
+    llm = LLM(REAL, max_num_seqs=256, max_seq_len=1024 + 32 + 16, block_size=256, seed=0)
+    rs = np.random.RandomState(5)
+    prompts = [rs.randint(0, REAL.vocab_size, n).tolist() for n in (1000, 1017, 777, 1024)]
+    outs = llm.generate(prompts, max_tokens=32, ignore_eos=True).result(timeout=300)
+    llm.stop()
+    assert [o.generated_tokens for o in outs] == [32] * 4
+    checked = total = 0
+    for p, o in zip(prompts, outs):
+        ref = reference_logits(llm.model, p + o.token_ids[:-1])[len(p) - 1:]
+        assert torch.isfinite(ref).all()
+        top2 = ref.topk(2, dim=-1)
+        margin = top2.values[:, 0] - top2.values[:, 1]
+        for i, tok in enumerate(o.token_ids):
+            total += 1
+            if margin[i] > 0.05:
+                assert tok == int(top2.indices[i, 0]), f"token {i} of prompt len {len(p)}"
+                checked += 1
+        del ref
+    print(f"checked {checked} of {total} tokens against the reference", flush=True)
+    assert checked >= 0.5 * total, checked
+
+
+def test_qwen3_0p6b_engine_full_workload_properties(gpu):
+    """The full 256 x 1024-in / 1024-out workload of the benchmark on the
+    graph-captured engine: every request yields exactly 1024 in-vocabulary
+    tokens (262,144 in all), and the first 8 tokens of every request equal
+    those of the eager (uncaptured, synchronous) engine on the same batch."""
+    print("case: Qwen3-0.6B 256 x 1024/1024 engine run", flush=True)
+    B, Lin, Lout = 256, 1024, 1024
+    rs = np.random.RandomState(0)
+    prompts = [rs.randint(0, REAL.vocab_size, Lin).tolist() for _ in range(B)]
+    llm = LLM(REAL, max_num_seqs=B, max_seq_len=Lin + Lout + 16, block_size=256, seed=0)
+    outs = llm.generate(prompts, max_tokens=Lout, ignore_eos=True).result(timeout=300)
+    llm.stop()
+    assert [o.generated_tokens for o in outs] == [Lout] * B
+    assert sum(o.generated_tokens for o in outs) == 262144
+    assert all(0 <= t < REAL.vocab_size for o in outs for t in o.token_ids)
+    assert llm.allocator.num_free == llm.allocator.num_blocks - 1  # every block returned
+    graphed = [o.token_ids[:8] for o in outs]
+    del llm, outs
+    torch.cuda.empty_cache()
+    print("case: eager engine, 256 x 1024/8", flush=True)
+    eager = LLM(REAL, max_num_seqs=B, max_seq_len=Lin + Lout + 16, block_size=256, seed=0,
+                use_graphs=False)
+    e_outs = eager.generate(prompts, max_tokens=8, ignore_eos=True).result(timeout=300)
+    eager.stop()
+    assert [o.token_ids for o in e_outs] == graphed
+    del eager
+    torch.cuda.empty_cache()

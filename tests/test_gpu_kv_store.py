@@ -129,3 +129,57 @@ def test_append_paged_through_c_abi(gpu):
     torch.cuda.synchronize()
     assert np.array_equal(bytes_of(kc_g), k_ref.view(np.uint8))
     assert np.array_equal(bytes_of(vc_g), v_ref.view(np.uint8))
+
+
+def test_check_mode_raises_index_error_like_index_copy(gpu, monkeypatch):
+    """With AAC_CHECK the store raises IndexError for every slot index_copy_
+    rejects (negative or >= rows), before anything is written; by default it
+    skips them (the padding convention), leaving those rows untouched."""
+    print("case: store error contract (AAC_CHECK on / off)", flush=True)
+    n, hkv, d, rows = 6, 2, 128, 16
+    kc = _sentinel_cache((rows // 4, 4, hkv, d), torch.bfloat16, gpu, 12)
+    before = kc.clone()
+    k = torch.ones(n, hkv, d, dtype=torch.bfloat16, device=gpu)
+    monkeypatch.setattr(fai, "_CHECK", True)
+    for bad in (-1, rows, rows + 40):
+        sm = torch.tensor([0, 1, 2, bad, 4, 5], dtype=torch.int64, device=gpu)
+        with pytest.raises(IndexError, match="out of bounds"):
+            fai.kv_store(k, k, kc, kc.clone(), sm)
+        cu = torch.tensor([0, n], dtype=torch.int32, device=gpu)
+        q = torch.ones(n, 4, d, dtype=torch.bfloat16, device=gpu)
+        with pytest.raises(IndexError, match="out of bounds"):
+            fai.varlen_prefill_with_kvcache(q, k, k, cu, n, kc, kc.clone(), sm)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, before)  # nothing was launched
+    monkeypatch.setattr(fai, "_CHECK", False)
+    sm = torch.tensor([0, -1, 2, rows, 4, -3], dtype=torch.int64, device=gpu)
+    fai.kv_store(k, k, kc, kc.clone(), sm)
+    torch.cuda.synchronize()
+    flat, ref = kc.view(rows, hkv, d), before.view(rows, hkv, d)
+    for r in range(rows):
+        want = torch.ones_like(flat[r]) if r in (0, 2, 4) else ref[r]
+        assert torch.equal(flat[r], want), r
+
+
+def test_padded_branch_store_is_one_kv_store(gpu):
+    """The padded prefill branch's per-slot copies (model/model.py:244-250)
+    as one kv_store through paged.padded_prefill_slot_mapping: bit-exact
+    against the copies made by torch slicing, untouched rows included."""
+    print("case: padded-branch store", flush=True)
+    B, T, hkv, d, lmax, nslot = 4, 300, 8, 128, 2064, 6
+    g = torch.Generator(device="cpu").manual_seed(13)
+    qkv = torch.randn(B, T, (16 + 2 * hkv) * d, generator=g).to(torch.bfloat16).to(gpu)
+    k = qkv[..., 16 * d:(16 + hkv) * d].contiguous().view(B, T, hkv, d)
+    v = qkv[..., (16 + hkv) * d:].view(B, T, hkv, d)  # strided view, as model/model.py:222
+    slots, lens = [5, 0, 3, 2], [300, 17, 0, 256]
+    kc = _sentinel_cache((nslot, lmax, hkv, d), torch.bfloat16, gpu, 14)
+    vc = _sentinel_cache((nslot, lmax, hkv, d), torch.bfloat16, gpu, 15)
+    kr, vr = kc.clone(), vc.clone()
+    for i, s in enumerate(slots):
+        kr[s, :lens[i]] = k[i, :lens[i]]
+        vr[s, :lens[i]] = v[i, :lens[i]]
+    sm = torch.from_numpy(paged.padded_prefill_slot_mapping(slots, lens, T, lmax)).to(gpu)
+    fai.kv_store(k.reshape(B * T, hkv, d), v.reshape(B * T, hkv, d), kc, vc, sm)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.view(torch.int16), kr.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), vr.view(torch.int16))

@@ -69,3 +69,102 @@ def test_wrappers_refuse_cpu_tensors_and_unsupported_features():
     with pytest.raises(NotImplementedError):
         fai.flash_attn_with_kvcache(q.view(4, 1, 16, 128), k, k, cache_seqlens=1,
                                     rotary_cos=torch.zeros(1))
+
+
+def test_slot_checks_raise_what_index_copy_raises():
+    """The engine's host-side slot checks reject exactly the indices the
+    reference's store, ``index_copy_`` (llm.py:171-174), rejects."""
+    rows = 4 * 8  # 4 blocks of 8
+    cache = torch.zeros(rows, 2)
+    for slots in ([0, 5, 31], [0, 32], [3, -1], [-40]):
+        t = torch.tensor(slots, dtype=torch.int64)
+        try:
+            cache.index_copy_(0, t, torch.ones(len(slots), 2))
+            torch_raises = False
+        except IndexError:
+            torch_raises = True
+        if torch_raises:
+            with pytest.raises(IndexError):
+                paged.check_slots(np.array(slots), rows)
+        else:
+            paged.check_slots(np.array(slots), rows)
+    bt = paged.pad_block_tables([[1, 3], [2]])
+    # a block id past the cache and a position past the table both raise
+    with pytest.raises(IndexError):
+        paged.build_prefill_metadata([9, 3], paged.pad_block_tables([[1, 4], [2]]), 8, "cpu",
+                                     num_cache_rows=rows)
+    with pytest.raises(IndexError):
+        paged.build_prefill_metadata([17, 3], bt, 8, "cpu", num_cache_rows=rows)
+    with pytest.raises(IndexError):
+        paged.decode_slot_mapping(bt, [3, 16], 8, num_cache_rows=rows)
+    cu, _, sm = paged.build_prefill_metadata([9, 3], bt, 8, "cpu", num_cache_rows=rows)
+    assert sm.tolist() == [8, 9, 10, 11, 12, 13, 14, 15, 24, 16, 17, 18]
+
+
+def test_padded_prefill_slot_mapping_matches_the_per_slot_loop():
+    """One store through the mapping writes what the padded branch's loop
+    ``cache[slot, :L] = k[i, :L]`` writes (model/model.py:244-250, with the
+    slice the TP twin uses, model/model_tp.py:218), byte for byte."""
+    B, T, hkv, d, lmax, nslot = 3, 7, 2, 4, 9, 5
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(B, T, hkv, d, generator=g)
+    slots, lens = [4, 0, 2], [7, 3, 0]
+    ref = torch.randn(nslot, lmax, hkv, d, generator=g)
+    got = ref.clone()
+    for i, s in enumerate(slots):
+        ref[s, :lens[i]] = k[i, :lens[i]]
+    sm = paged.padded_prefill_slot_mapping(slots, lens, T, lmax)
+    assert sm.shape == (B * T,) and sm.dtype == np.int64
+    keep = sm >= 0
+    got.view(-1, hkv, d).index_copy_(0, torch.from_numpy(sm[keep]), k.reshape(B * T, hkv, d)[keep])
+    assert torch.equal(got, ref)
+    with pytest.raises(ValueError):
+        paged.padded_prefill_slot_mapping([0], [8], 7, lmax)
+
+
+def _pick_config(m, n, k):
+    """aac_gemm_nt's tiling choice (csrc/gemm.hip pick_config) restated:
+    (M tiles, N tiles, K per stage) of configurations 1..6."""
+    cfg = {1: (2, 2, 128), 2: (1, 1, 256), 3: (2, 1, 128), 4: (1, 2, 128), 5: (2, 1, 256),
+           6: (2, 2, 128)}
+    cd = lambda a, b: -(-a // b)  # noqa: E731
+    if n % 64 == 0 and k % 128 == 0 and cd(m, 64) * (n // 64) >= 128:
+        return 6
+    if n % 32 == 0 and k % 256 == 0 and cd(m, 32) * (n // 32) >= 256:
+        return 2
+    best, best_tiles = 0, -1
+    for c in (1, 3, 4, 2):
+        tc = 32 * cfg[c][1]
+        if n % tc or k % cfg[c][2]:
+            continue
+        tiles = cd(m, 32 * cfg[c][0]) * (n // tc)
+        if tiles >= 256:
+            return c
+        if tiles > best_tiles:
+            best, best_tiles = c, tiles
+    return best
+
+
+def test_linear_supported_agrees_with_the_tiling_choice():
+    from awesome_acceleration_amd import fused
+    for m in (1, 33, 256, 700):
+        for n in (32, 64, 96, 1024, 3072, 4096, 5120, 100):
+            for k in (64, 128, 192, 256, 1024, 3072, 5120, 320):
+                assert fused.linear_supported(m, n, k) == (_pick_config(m, n, k) != 0), (m, n, k)
+    assert fused.rmsnorm_supported(1024) and fused.rmsnorm_supported(4096)
+    assert not fused.rmsnorm_supported(5120) and not fused.rmsnorm_supported(768)
+
+
+def test_engine_rejects_a_request_larger_than_the_block_pool():
+    """A request whose reserved blocks exceed the whole pool is refused at
+    submission (it could never be admitted)."""
+    from awesome_acceleration_amd.llm import LLM
+    llm = LLM.__new__(LLM)  # the submission checks only, no model or device
+    llm.max_seq_len, llm.block_size = 1024, 64
+    llm.allocator = paged.BlockAllocator(4 + 1)  # 4 blocks plus the scratch block
+    llm._ensure_loop = lambda: None
+    llm._request_queue = __import__("queue").Queue()
+    with pytest.raises(ValueError, match="KV blocks"):
+        llm.generate([[1] * 200], max_tokens=100)  # 300 tokens -> 5 blocks of 64
+    llm.generate([[1] * 200], max_tokens=56)  # 256 tokens -> 4 blocks: accepted
+    assert llm._request_queue.qsize() == 1
