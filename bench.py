@@ -64,15 +64,19 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_PROFILE = "profiles/decode_256seq_ctx1k-2k_bf16_traffic.md"
+TRAFFIC_PREFILL = "profiles/prefill_8x1024_bf16_traffic.md"
+TRAFFIC_DECODE_LONG = "profiles/decode_long_64seq_ctx16k-32k_bf16_traffic.md"
+TRAFFIC_KV_EXPORT = "profiles/kv_export_2048tok_28layers_bf16_traffic.md"
 
 
-def measured_traffic():
-    """HBM bytes per decode launch from the committed counter summary
-    (FETCH_SIZE/WRITE_SIZE scaled by a plain copy), or None."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_PROFILE)
+def measured_traffic(profile=TRAFFIC_PROFILE, key="traffic_bytes_per_launch"):
+    """Bytes per launch moved between L2 and memory, from a committed counter
+    summary (FETCH_SIZE / WRITE_SIZE scaled by the same counters on a plain
+    copy of known size), or None when the summary is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), profile)
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(key + ":"):
                 return int(line.split(":")[1])
     except OSError:
         pass
@@ -102,7 +106,8 @@ def parse():
     p.add_argument("--e2e-seqs", type=int, default=256)
     p.add_argument("--e2e-in", type=int, default=1024)
     p.add_argument("--e2e-out", type=int, default=1024)
-    p.add_argument("--only", choices=["decode", "decode_slot", "decode_long", "tp2_rank", "kv_transfer",
+    p.add_argument("--only", choices=["decode", "decode_fp32_small", "decode_slot", "decode_long",
+                                      "tp2_rank", "kv_transfer",
                                       "prefill", "prefill_long", "e2e"],
                    default=None,
                    help="run one leg only (for profiling)")
@@ -208,6 +213,47 @@ def bench_decode(torch, fai, dev, args, hq=16, hkv=8):
 
 
 # ----------------------------------------------------------------------------
+# the CPU-runnable fp32 decode case: 4 seqs, contexts {17, 64, 200, 511}
+# ----------------------------------------------------------------------------
+def bench_decode_fp32_small(torch, fai, dev, args):
+    """The fp32 single-layer decode of the golden fixture's shape (batch 4,
+    16 / 8 heads, contexts 17 / 64 / 200 / 511 after the store, block 256,
+    blocks from a permuted 16-block pool): store + attend through
+    flash_attn_with_kvcache on the GPU, per call."""
+    B, hq, hkv, d, bs, pool = 4, 16, 8, 128, 256, 16
+    ctx = np.array([17, 64, 200, 511], np.int32)
+    rs = np.random.RandomState(args.seed)
+    perm = rs.permutation(pool).astype(np.int32)
+    bt = np.zeros((B, 2), np.int32)
+    k0 = 0
+    for b in range(B):
+        n = -(-int(ctx[b]) // bs)
+        bt[b, :n] = perm[k0:k0 + n]
+        k0 += n
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    kc = torch.randn((pool, bs, hkv, d), generator=g, device=dev)
+    vc = torch.randn((pool, bs, hkv, d), generator=g, device=dev)
+    q = torch.randn((B, 1, hq, d), generator=g, device=dev)
+    kn = torch.randn((B, 1, hkv, d), generator=g, device=dev)
+    vn = torch.randn((B, 1, hkv, d), generator=g, device=dev)
+    bt_g, sl_g = torch.from_numpy(bt).to(dev), torch.from_numpy(ctx - 1).to(dev)
+
+    def step():
+        return fai.flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=sl_g,
+                                           block_table=bt_g, max_context_len=int(ctx.max()))
+
+    for _ in range(args.warmup):
+        step()
+    warm(torch, [step], min(args.warmup_seconds, 0.5))
+    t = launch_avg(torch, step, args.steps)
+    nbytes = int(ctx.sum()) * hkv * d * 4 * 2 + 2 * B * hq * d * 4 + 4 * B * hkv * d * 4
+    return {"workload": "fp32 paged decode store+attend, 4 seqs, 16 q / 8 kv heads, head_dim 128, "
+                        "contexts {17, 64, 200, 511}, block 256, permuted 16-block pool",
+            "us_per_step": round(t * 1e6, 2), "bytes_per_step": nbytes,
+            "achieved": round(nbytes / t / 1e9, 2), "unit": "GB/s", "ctx": ctx}
+
+
+# ----------------------------------------------------------------------------
 # the same decode through the reference's own slot layout: caches
 # [slots, max_seq_len, Hkv, D] picked by cache_batch_idx (model/model.py:233-240)
 # ----------------------------------------------------------------------------
@@ -263,7 +309,8 @@ def bench_decode_long(torch, fai, dev, args):
         "us_per_call": round(t * 1e6, 2),
         "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "bytes_per_call": attend_bytes,
-                     "traffic": None},
+                     "traffic": measured_traffic(TRAFFIC_DECODE_LONG),
+                     "traffic_source": TRAFFIC_DECODE_LONG},
     }
 
 
@@ -301,7 +348,8 @@ def bench_kv_transfer(torch, dev, args):
         "us_export": round(t_ex * 1e6, 2), "us_import": round(t_im * 1e6, 2),
         "roofline": {"bound": "hbm", "achieved": round(moved / t_ex / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(moved / t_ex / 1e9 / HBM_PEAK_GBS, 4),
-                     "bytes_per_call": moved, "traffic": None},
+                     "bytes_per_call": moved, "traffic": measured_traffic(TRAFFIC_KV_EXPORT),
+                     "traffic_source": TRAFFIC_KV_EXPORT},
         "import_GBs": round(moved / t_im / 1e9, 2),
         "request_to_pinned_host_ms": round(t_host * 1e3, 3),
         "request_to_pinned_host_GBs": round(moved / 2 / t_host / 1e9, 2),
@@ -409,9 +457,140 @@ def bench_e2e(torch, args):
 
 
 # ----------------------------------------------------------------------------
-# CPU baseline: the oracle on a bounded sample of the decode workload
+# CPU baselines: the reference's semantics in fp32 torch on the host cores
+# (oracle/torch_path.py, oracle/qwen3_ref.py), 3 warm-ups then the median of 5
 # ----------------------------------------------------------------------------
-def cpu_baseline(x, reps=12, seed=1):
+def _median_time(fn, warmup=3, reps=5):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), ts
+
+
+def _host_fill(torch, shape, dtype, seed):
+    """A host tensor of N(0,1) values (a 4 Mi-value draw repeated; seconds to
+    fill gigabytes, and the values do not change the work)."""
+    g = torch.Generator().manual_seed(seed)
+    base = torch.randn(1 << 22, generator=g).to(dtype)
+    t = torch.empty(shape, dtype=dtype)
+    flat = t.view(-1)
+    for i in range(0, flat.numel(), base.numel()):
+        m = min(base.numel(), flat.numel() - i)
+        flat[i:i + m] = base[:m]
+    return t
+
+
+def _paged_tables(ctx, bs, rs):
+    need = [int(-(-int(c) // bs)) for c in ctx]
+    pool = sum(need)
+    perm = rs.permutation(pool)
+    bt = np.zeros((len(ctx), max(need)), np.int64)
+    k0 = 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[k0:k0 + n]
+        k0 += n
+    return bt, pool
+
+
+def cpu_decode_baseline(torch, ctx, hq, hkv, label, threads, dtype=None, d=128, bs=256, seed=3):
+    """Paged decode store+attend (model/model.py:233-241) on the host:
+    oracle.torch_path.decode_store_attend in fp32 on bf16-valued caches (or
+    ``dtype``), the same contexts, 16/8 or 32/8 heads, block 256."""
+    from oracle import torch_path as tp
+    dtype = dtype or torch.bfloat16
+    rs = np.random.RandomState(seed)
+    B = len(ctx)
+    bt, pool = _paged_tables(ctx, bs, rs)
+    kc = _host_fill(torch, (pool, bs, hkv, d), dtype, seed)
+    vc = _host_fill(torch, (pool, bs, hkv, d), dtype, seed + 1)
+    q = _host_fill(torch, (B, hq, d), dtype, seed + 2)
+    kn = _host_fill(torch, (B, hkv, d), dtype, seed + 3)
+    vn = _host_fill(torch, (B, hkv, d), dtype, seed + 4)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        med, ts = _median_time(lambda: tp.decode_store_attend(q, kn, vn, kc, vc, bt, ctx - 1,
+                                                              d ** -0.5))
+    finally:
+        torch.set_num_threads(prev)
+    esz = torch.tensor([], dtype=dtype).element_size()
+    nbytes = int(ctx.sum()) * hkv * d * esz * 2 + 2 * B * hq * d * esz + 4 * B * hkv * d * esz
+    return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                seconds_per_step=round(med, 4), bytes_per_step=nbytes,
+                sample=f"{label}: store+attend of one decode step (oracle.torch_path, fp32 torch "
+                       f"on {str(dtype).split('.')[-1]}-valued caches, {threads} host threads), "
+                       f"median of 5 after 3 warm-ups ({sum(ts):.1f} s timed)")
+
+
+def cpu_prefill_baseline(torch, nseq, L, hq, hkv, threads, d=128, bs=256, seed=4):
+    """Varlen causal prefill store+attend (llm.py:171-184) on the host:
+    index_copy_ into a shuffled paged cache, then torch SDPA per segment in
+    fp32 on bf16-valued q/k/v."""
+    from oracle import torch_path as tp
+    N = nseq * L
+    rs = np.random.RandomState(seed)
+    nb = -(-L // bs)
+    perm = rs.permutation(nseq * nb)
+    pos = np.arange(N) % L
+    seg = np.arange(N) // L
+    sm = torch.from_numpy(perm.reshape(nseq, nb)[seg, pos // bs] * bs + pos % bs)
+    q = _host_fill(torch, (N, hq, d), torch.bfloat16, seed)
+    k = _host_fill(torch, (N, hkv, d), torch.bfloat16, seed + 1)
+    v = _host_fill(torch, (N, hkv, d), torch.bfloat16, seed + 2)
+    kc = torch.zeros((nseq * nb, bs, hkv, d), dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    cu = list(range(0, N + 1, L))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        med, ts = _median_time(lambda: tp.prefill_store_attend(q, k, v, cu, kc, vc, sm,
+                                                               d ** -0.5))
+    finally:
+        torch.set_num_threads(prev)
+    flops = 4 * hq * d * nseq * (L * (L + 1) // 2)
+    return dict(value=round(flops / med / 1e12, 4), unit="TFLOP/s", cores=threads, kind="port",
+                seconds_per_call=round(med, 4),
+                sample=f"varlen causal prefill {nseq} x {L}, {hq}/{hkv} heads: index_copy_ store "
+                       f"+ torch SDPA per segment (oracle.torch_path, fp32 on bf16-valued inputs, "
+                       f"{threads} host threads), median of 5 after 3 warm-ups "
+                       f"({sum(ts):.1f} s timed)")
+
+
+def cpu_e2e_small_run(torch, threads, n_req=8, n_in=128, n_out=32, seed=5):
+    """A complete small generation run on the host: random-init Qwen3-0.6B
+    (oracle.qwen3_ref, fp32 torch, the reference's slot caches, packed varlen
+    prefill then batched greedy decode steps), n_req requests x n_in random
+    tokens, n_out output tokens each (ignore_eos)."""
+    from awesome_acceleration_amd.qwen3 import Qwen3Config
+    from oracle.qwen3_ref import Qwen3Ref
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        cfg = Qwen3Config()
+        ref = Qwen3Ref.random(cfg, seed=seed, tiled=True)
+        rs = np.random.RandomState(seed)
+        prompts = [rs.randint(0, cfg.vocab_size, n_in).tolist() for _ in range(n_req)]
+        ref.generate(prompts[:2], max_tokens=2, max_seq_len=n_in + n_out + 16)  # warm-up
+        t0 = time.perf_counter()
+        outs = ref.generate(prompts, max_tokens=n_out, max_seq_len=n_in + n_out + 16)
+        el = time.perf_counter() - t0
+    finally:
+        torch.set_num_threads(prev)
+    gen = sum(len(o) for o in outs)
+    return dict(value=round(gen / el, 2), unit="output tok/s", cores=threads, kind="port",
+                total_tok_s=round((gen + n_req * n_in) / el, 2), seconds=round(el, 3),
+                sample=f"complete run of {n_req} requests x {n_in} random input tokens, {n_out} "
+                       f"greedy output tokens each, random-init Qwen3-0.6B in fp32 torch "
+                       f"(oracle.qwen3_ref: packed prefill + batched decode over slot caches) on "
+                       f"{threads} host threads; the full 256 x 1024/1024 workload is not run on "
+                       f"the host (hours)")
+
+
+def oracle_1core(x, reps=12, seed=1):
     """The oracle's store-then-attend over the same decode shape (all 256
     sequences, the same context lengths), single-threaded; the median of
     ``reps`` runs (about 10 s of CPU work)."""
@@ -553,6 +732,8 @@ def main():
     res = {}
     if args.only in (None, "decode"):
         res["decode"] = bench_decode(torch, fai, dev, args)
+    if args.only in (None, "decode_fp32_small"):
+        res["decode_fp32_small"] = bench_decode_fp32_small(torch, fai, dev, args)
     if args.only in (None, "decode_slot") and not args.no_slot:
         res["decode_slot"] = bench_decode_slot(torch, fai, dev, args)
         torch.cuda.empty_cache()
@@ -586,15 +767,14 @@ def main():
     if args.only in (None, "e2e") and not args.no_e2e:
         res["e2e"] = bench_e2e(torch, args)
     if args.only is not None:
-        if args.only == "decode":
-            # calibration for counter-based traffic: a plain 1 GiB device copy
-            # (1 GiB read + 1 GiB written) in the same process
-            src = torch.empty(1 << 29, dtype=torch.int16, device=dev)
-            dst = torch.empty_like(src)
-            for _ in range(3):
-                dst.copy_(src)
-            torch.cuda.synchronize()
-        print(json.dumps({k: {kk: vv for kk, vv in v.items() if kk != "x"}
+        # calibration for counter-based traffic: a plain 1 GiB device copy
+        # (1 GiB read + 1 GiB written) in the same process
+        src = torch.empty(1 << 29, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({k: {kk: vv for kk, vv in v.items() if kk not in ("x", "ctx")}
                           for k, v in res.items()}, default=float))
         return
     dec = res["decode"]
@@ -642,7 +822,11 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(pf["tflops"], 2),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pf["tflops"] / BF16_PEAK_TFLOPS, 4),
-                         "flops_per_launch": pf["flops"], "traffic": None},
+                         "flops_per_launch": pf["flops"],
+                         "traffic": measured_traffic(TRAFFIC_PREFILL),
+                         "traffic_with_store": measured_traffic(TRAFFIC_PREFILL,
+                                                                "traffic_bytes_per_launch_store"),
+                         "traffic_source": TRAFFIC_PREFILL},
         }
     if "decode_long" in res:
         line["decode_long"] = res["decode_long"]
@@ -656,11 +840,38 @@ def main():
         line["kv_transfer"] = res["kv_transfer"]
     if "e2e" in res:
         line["e2e"] = res["e2e"]
+    if "decode_fp32_small" in res:
+        line["decode_fp32_small"] = {k: v for k, v in res["decode_fp32_small"].items()
+                                     if k != "ctx"}
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(dec["x"])
-        if "e2e" in line:  # the end-to-end decode step on the host, same contexts
-            line["e2e"]["cpu_baseline"] = cpu_e2e_baseline(
-                torch, dec["x"]["ctx"], threads=min(len(os.sched_getaffinity(0)), 16))
+        from oracle.torch_path import cpu_threads
+        n = cpu_threads()
+        line["cpu_baseline"] = cpu_decode_baseline(
+            torch, dec["x"]["ctx"], 16, 8, f"256 seqs x context U[1024,2047] (the same "
+            f"{int(dec['x']['ctx'].sum())} context tokens), 16/8 heads, block 256", n)
+        line["cpu_baseline"]["host_cpus_visible"] = len(os.sched_getaffinity(0))
+        line["cpu_baseline"]["oracle_1core"] = oracle_1core(dec["x"], reps=5)
+        if "decode_fp32_small" in res:
+            small = cpu_decode_baseline(torch, res["decode_fp32_small"]["ctx"], 16, 8,
+                                        "4 seqs x contexts {17, 64, 200, 511}", n,
+                                        dtype=torch.float32)
+            line["decode_fp32_small"]["cpu_baseline"] = small
+            line["decode_fp32_small"]["vs_cpu"] = round(
+                small["seconds_per_step"] * 1e6 / line["decode_fp32_small"]["us_per_step"], 1)
+        if "prefill" in line:
+            line["prefill"]["cpu_baseline"] = cpu_prefill_baseline(
+                torch, args.prefill_seqs, args.prefill_len, 16, 8, n)
+        if "decode_long" in line:
+            ctx_long = np.random.RandomState(args.seed).randint(16384, 32769, 64).astype(np.int32)
+            line["decode_long"]["cpu_baseline"] = cpu_decode_baseline(
+                torch, ctx_long[:16], 32, 8, "the first 16 of the 64 sequences (context "
+                f"{int(ctx_long[:16].sum())} tokens), 32/8 heads, block 256", n)
+        if "e2e" in line:
+            line["e2e"]["cpu_baseline"] = cpu_e2e_small_run(torch, n)
+            # the end-to-end decode step at the workload's batch, extrapolated
+            # from one layer (the full run would take hours on the host)
+            line["e2e"]["cpu_decode_step_extrapolated"] = cpu_e2e_baseline(
+                torch, dec["x"]["ctx"], threads=n)
             line["e2e"]["vs_cpu"] = round(line["e2e"]["output_tok_s"] /
                                           line["e2e"]["cpu_baseline"]["value"], 1)
     print(json.dumps(line))

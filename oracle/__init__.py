@@ -25,3 +25,6 @@ How each function is pinned is documented in ``oracle/attention.py``'s module
 docstring; none is "parity unpinned".
 """
 from .attention import *  # noqa: F401,F403
+
+# The fp32 Qwen3 model / engine-loop restatement (oracle/qwen3_ref.py) is
+# imported on demand: ``from oracle.qwen3_ref import Qwen3Ref``.

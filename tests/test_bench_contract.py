@@ -29,9 +29,9 @@ def test_decode_step_bytes():
     assert step == attend + 2 * 4 * 8 * 128 * 2 * 2
 
 
-def test_cpu_baseline_reports_a_port_on_one_core():
+def test_oracle_1core_reports_a_port_on_one_core():
     ctx = np.array([5, 300, 1], np.int32)
-    r = bench.cpu_baseline(dict(ctx=ctx, hq=4, hkv=2, d=128, bs=256), reps=1)
+    r = bench.oracle_1core(dict(ctx=ctx, hq=4, hkv=2, d=128, bs=256), reps=1)
     assert r["kind"] == "port" and r["cores"] == 1 and r["unit"] == "GB/s"
     assert r["value"] > 0 and r["seconds_per_step"] >= 0
     assert "3 sequences (306 context tokens)" in r["sample"]
@@ -44,3 +44,22 @@ def test_cpu_e2e_baseline_runs_the_layer_on_the_host():
                                d=16, layers=2, vocab=50)
     assert r["unit"] == "output tok/s" and r["kind"] == "port" and r["cores"] == 2
     assert r["value"] > 0 and "3 sequences (context 3-40" in r["sample"]
+
+
+def test_cpu_path_baselines_run_on_the_host_threads():
+    """The fp32 torch store+attend legs (decode, prefill) and the complete
+    small engine run report a rate, the threads used and what was timed."""
+    import torch
+    ctx = np.array([5, 300, 1, 77], np.int32)
+    r = bench.cpu_decode_baseline(torch, ctx, 4, 2, "tiny", threads=2)
+    assert r["unit"] == "GB/s" and r["cores"] == 2 and r["kind"] == "port" and r["value"] > 0
+    assert r["bytes_per_step"] == int(ctx.sum()) * 2 * 128 * 2 * 2 + 2 * 4 * 4 * 128 * 2 + \
+        4 * 4 * 2 * 128 * 2
+    p = bench.cpu_prefill_baseline(torch, 2, 300, 4, 2, threads=2)
+    assert p["unit"] == "TFLOP/s" and p["value"] > 0 and "2 x 300" in p["sample"]
+
+
+def test_traffic_summaries_are_read_from_profiles():
+    # the decode summary is committed; a missing file reads as None
+    assert bench.measured_traffic() and bench.measured_traffic() > 1.6e9
+    assert bench.measured_traffic("profiles/no_such_file.md") is None

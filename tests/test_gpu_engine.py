@@ -1,7 +1,7 @@
-"""The continuous-batching engine on the HIP kernels against an independent
-fp32 torch forward of the same random Qwen3 weights (teacher-forced over the
-prompt plus the generated tokens, attention by torch SDPA with causal mask and
-repeat-interleaved KV heads -- the textbook Qwen3 layer of model/model.py).
+"""The continuous-batching engine on the HIP kernels against the fp32
+restatement of the reference model (oracle.qwen3_ref, pinned to transformers'
+Qwen3) with the same random weights, teacher-forced over the prompt plus the
+generated tokens.
 
 Each generated token must be the reference argmax wherever the reference's
 top-2 logit margin exceeds the bf16 noise floor; graph-captured decode steps
@@ -9,10 +9,10 @@ must reproduce the eager engine token for token."""
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
 from awesome_acceleration_amd.llm import LLM
 from awesome_acceleration_amd.qwen3 import Qwen3Config
+from oracle.qwen3_ref import Qwen3Ref
 
 pytestmark = pytest.mark.gpu
 
@@ -21,44 +21,18 @@ CFG = Qwen3Config(vocab_size=2048, hidden_size=512, intermediate_size=1024, num_
                   max_position_embeddings=4096)
 
 
+_REFS = {}
+
+
 def reference_logits(model, ids):
-    """fp32 forward over one full sequence; returns logits [T, vocab]."""
-    cfg = model.cfg
-    dev = model.device
-    T = len(ids)
-    f = lambda t: t.float()  # noqa: E731
-    eps = cfg.rms_norm_eps
-
-    def norm(x, w):
-        return f(w) * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
-
-    pos = torch.arange(T, device=dev)
-    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, 128, 2, device=dev).float() / 128))
-    fr = torch.outer(pos.float(), inv)
-    emb = torch.cat((fr, fr), -1)
-    cos, sin = emb.cos()[:, None], emb.sin()[:, None]
-
-    def rope(x):
-        return x * cos + torch.cat((-x[..., 64:], x[..., :64]), -1) * sin
-
-    h = f(model.embed)[torch.tensor(ids, device=dev)]
-    hq, hkv, d = model.hq, model.hkv, model.d
-    for L in model.layers:
-        x = norm(h, L["ln1"])
-        qkv = x @ f(L["qkv"]).T
-        q = qkv[:, :hq * d].view(T, hq, d)
-        k = qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
-        v = qkv[:, (hq + hkv) * d:].view(T, hkv, d)
-        q, k = rope(norm(q, L["q_norm"])), rope(norm(k, L["k_norm"]))
-        g = hq // hkv
-        a = F.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1).repeat_interleave(g, 0),
-                                           v.transpose(0, 1).repeat_interleave(g, 0), is_causal=True)
-        h = h + a.transpose(0, 1).reshape(T, -1) @ f(L["o"]).T
-        x = norm(h, L["ln2"])
-        gu = x @ f(L["gate_up"]).T
-        I = cfg.intermediate_size
-        h = h + (F.silu(gu[:, :I]) * gu[:, I:]) @ f(L["down"]).T
-    return norm(h, model.norm) @ f(model.embed).T
+    """fp32 forward over one full sequence with the engine's weights; returns
+    logits [T, vocab].  The restatement (oracle.qwen3_ref) is pinned to
+    transformers' Qwen3 in tests/test_oracle_pins.py."""
+    key = id(model)
+    if key not in _REFS:
+        _REFS.clear()
+        _REFS[key] = Qwen3Ref.from_model(model)
+    return _REFS[key].logits(ids)
 
 
 def _prompts(n, seed):

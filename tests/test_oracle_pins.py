@@ -327,3 +327,143 @@ def test_kv_export_import_round_trip_and_relabelling_over_a_permuted_pool():
     s2 = sentinel.copy()
     oracle.kv_import(exp, s2, bad, length)
     assert (s2[:, :, bt[2]] == 7.0).all()  # the skipped block keeps its bytes
+
+
+# ---------------------------------------------------------------------------
+# The Qwen3 model / engine-loop restatement and the product's RMSNorm / RoPE
+# against transformers' independent Qwen3 implementation (CPU, fp32 / bf16)
+# ---------------------------------------------------------------------------
+def _hf_tiny(ref):
+    """transformers' Qwen3ForCausalLM carrying the weights of ``ref``."""
+    from transformers import Qwen3Config as HC, Qwen3ForCausalLM as HM
+    c = ref.cfg
+    hc = HC(vocab_size=c.vocab_size, hidden_size=c.hidden_size,
+            intermediate_size=c.intermediate_size, num_hidden_layers=c.num_hidden_layers,
+            num_attention_heads=c.num_attention_heads, num_key_value_heads=c.num_key_value_heads,
+            head_dim=c.head_dim, max_position_embeddings=c.max_position_embeddings,
+            rope_theta=c.rope_theta, rms_norm_eps=c.rms_norm_eps, tie_word_embeddings=True,
+            attn_implementation="eager")
+    hm = HM(hc).eval()
+    qs, ks, I = c.num_attention_heads * c.head_dim, c.num_key_value_heads * c.head_dim, \
+        c.intermediate_size
+    sd = {"model.embed_tokens.weight": ref.embed, "model.norm.weight": ref.norm,
+          "lm_head.weight": ref.embed}
+    for i, L in enumerate(ref.layers):
+        p = f"model.layers.{i}."
+        sd.update({p + "self_attn.q_proj.weight": L["qkv"][:qs],
+                   p + "self_attn.k_proj.weight": L["qkv"][qs:qs + ks],
+                   p + "self_attn.v_proj.weight": L["qkv"][qs + ks:],
+                   p + "self_attn.o_proj.weight": L["o"],
+                   p + "self_attn.q_norm.weight": L["q_norm"],
+                   p + "self_attn.k_norm.weight": L["k_norm"],
+                   p + "mlp.gate_proj.weight": L["gate_up"][:I],
+                   p + "mlp.up_proj.weight": L["gate_up"][I:],
+                   p + "mlp.down_proj.weight": L["down"],
+                   p + "input_layernorm.weight": L["ln1"],
+                   p + "post_attention_layernorm.weight": L["ln2"]})
+    hm.load_state_dict(sd, strict=True)
+    return hm
+
+
+def test_qwen3_restatement_matches_transformers():
+    """oracle.qwen3_ref (the engine-token checker and the e2e CPU baseline)
+    against transformers' Qwen3: full-sequence logits to fp32 rounding, and
+    the slot-cache engine loop (packed varlen prefill, batched decode steps)
+    reproduces transformers' greedy continuation of every prompt."""
+    from awesome_acceleration_amd.qwen3 import Qwen3Config
+    from oracle.qwen3_ref import Qwen3Ref
+    cfg = Qwen3Config(vocab_size=512, hidden_size=256, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                      head_dim=128, max_position_embeddings=1024)
+    ref = Qwen3Ref.random(cfg, seed=1, std=0.05)
+    for L in ref.layers:  # non-trivial norm weights, so a dropped weight fails
+        for name in ("ln1", "ln2", "q_norm", "k_norm"):
+            L[name] = 1 + 0.2 * torch.randn(L[name].shape, generator=torch.Generator().manual_seed(7))
+    hm = _hf_tiny(ref)
+    ids = torch.randint(0, 512, (41,), generator=torch.Generator().manual_seed(0))
+    with torch.no_grad():
+        a, b = ref.logits(ids.tolist()), hm(ids[None]).logits[0]
+    assert float((a - b).abs().max()) <= 1e-4 * float(b.abs().max())
+    prompts = [ids[:5].tolist(), ids[:23].tolist(), ids[9:41].tolist()]
+    toks = ref.generate(prompts, max_tokens=10, max_seq_len=64)
+    for p, t in zip(prompts, toks):
+        with torch.no_grad():
+            g = hm.generate(torch.tensor([p]), max_new_tokens=10, do_sample=False,
+                            eos_token_id=None, pad_token_id=0)[0, len(p):].tolist()
+        assert t == g
+
+
+def test_product_rmsnorm_and_rope_match_transformers():
+    """The product's torch RMSNorm and RoPE tables/rotation (the expressions
+    the fused HIP kernels are checked against to an ulp) are bit-identical to
+    transformers' Qwen3RMSNorm, Qwen3RotaryEmbedding and apply_rotary_pos_emb
+    on bf16 activations (model/model.py:47-52, :64-99)."""
+    from transformers import Qwen3Config as HC
+    from transformers.models.qwen3 import modeling_qwen3 as mq
+    from awesome_acceleration_amd.qwen3 import Rope, rms_norm
+    g = torch.Generator().manual_seed(3)
+    x = (3 * torch.randn(50, 8, 128, generator=g)).to(torch.bfloat16)
+    w = (1 + 0.3 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    hn = mq.Qwen3RMSNorm(128, eps=1e-6)
+    hn.weight.data = w.clone()
+    with torch.no_grad():
+        assert torch.equal(rms_norm(x, w, 1e-6), hn(x))
+    hc = HC(head_dim=128, rope_theta=1e6, max_position_embeddings=4096, hidden_size=1024,
+            num_attention_heads=8)
+    rot = mq.Qwen3RotaryEmbedding(hc)
+    pos = torch.randint(0, 4096, (50,), generator=g)
+    cos, sin = rot(x, pos[None])
+    mine = Rope(128, 4096, 1e6, "cpu", torch.bfloat16)
+    assert torch.equal(mine.cos[pos], cos[0]) and torch.equal(mine.sin[pos], sin[0])
+    q = x.transpose(0, 1)[None]  # [1, H, T, D]
+    hq, _ = mq.apply_rotary_pos_emb(q, q, cos, sin)
+    assert torch.equal(mine.apply(x, pos), hq[0].transpose(0, 1))
+
+
+def test_torch_path_restatement_matches_the_oracle():
+    """oracle.torch_path (bench.py's fp32 host baseline for configs 1-4)
+    against the float64 oracle: stores bit-exact (the same index_copy_ op),
+    attention within fp32 rounding, on the config-1 decode shape (fp32,
+    contexts 17/64/200/511, block 256, permuted 16-block pool) and a ragged
+    GQA-2 causal prefill."""
+    from oracle import torch_path as tp
+    rs = np.random.RandomState(0)
+    B, hq, hkv, d, bs = 4, 16, 8, 128, 256
+    ctx = np.array([17, 64, 200, 511])
+    perm = rs.permutation(16)
+    bt = np.zeros((B, 2), np.int64)
+    k0 = 0
+    for b in range(B):
+        n = -(-int(ctx[b]) // bs)
+        bt[b, :n] = perm[k0:k0 + n]
+        k0 += n
+    kc = rs.standard_normal((16, bs, hkv, d)).astype(np.float32)
+    vc = rs.standard_normal((16, bs, hkv, d)).astype(np.float32)
+    q = rs.standard_normal((B, hq, d)).astype(np.float32)
+    kn = rs.standard_normal((B, hkv, d)).astype(np.float32)
+    vn = rs.standard_normal((B, hkv, d)).astype(np.float32)
+    kr, vr = kc.copy(), vc.copy()
+    ref, _ = oracle.decode_append_attend(q, kr, vr, kn, vn, bt, ctx - 1, bs)
+    kt, vt = torch.from_numpy(kc.copy()), torch.from_numpy(vc.copy())
+    out = tp.decode_store_attend(torch.from_numpy(q), torch.from_numpy(kn), torch.from_numpy(vn),
+                                 kt, vt, bt, ctx - 1, d ** -0.5)
+    assert np.array_equal(kt.numpy(), kr) and np.array_equal(vt.numpy(), vr)
+    assert np.abs(out.double().numpy() - ref).max() <= 1e-5
+    # prefill: three segments (one empty), 16 / 8 heads, store through a shuffled slot map
+    lens = [37, 0, 129]
+    n = sum(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q = rs.standard_normal((n, hq, d)).astype(np.float32)
+    k = rs.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rs.standard_normal((n, hkv, d)).astype(np.float32)
+    sm = rs.permutation(4 * 64)[:n].astype(np.int64)
+    kc = rs.standard_normal((4, 64, hkv, d)).astype(np.float32)
+    kr, kt = kc.copy(), torch.from_numpy(kc.copy())
+    vr, vt = kc.copy() + 1, torch.from_numpy(kc.copy() + 1)
+    oracle.kv_store(kr, k, sm)
+    oracle.kv_store(vr, v, sm)
+    out = tp.prefill_store_attend(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                                  cu, kt, vt, torch.from_numpy(sm), d ** -0.5)
+    assert np.array_equal(kt.numpy(), kr) and np.array_equal(vt.numpy(), vr)
+    ref = oracle.varlen_attention(q, k, v, cu)
+    assert np.abs(out.double().numpy() - ref).max() <= 1e-5
