@@ -336,6 +336,11 @@ def bench_kv_transfer(torch, dev, args):
 
     t_ex = timed(lambda: kt.kv_export(st, bt, length, out=buf))
     t_im = timed(lambda: kt.kv_import(buf, st, bt, length))
+    # a plain device-to-device copy of the same bytes (torch / the HIP runtime's
+    # copy kernel): the ceiling a gather of 512 KiB runs can approach
+    buf2 = torch.empty_like(buf)
+    t_cp = timed(lambda: buf2.copy_(buf))
+    del buf2
     t0 = time.perf_counter()
     for _ in range(3):
         kt.export_request_kv(st, bt, length, length)
@@ -351,6 +356,7 @@ def bench_kv_transfer(torch, dev, args):
                      "bytes_per_call": moved, "traffic": measured_traffic(TRAFFIC_KV_EXPORT),
                      "traffic_source": TRAFFIC_KV_EXPORT},
         "import_GBs": round(moved / t_im / 1e9, 2),
+        "copy_GBs": round(moved / t_cp / 1e9, 2),
         "request_to_pinned_host_ms": round(t_host * 1e3, 3),
         "request_to_pinned_host_GBs": round(moved / 2 / t_host / 1e9, 2),
     }
