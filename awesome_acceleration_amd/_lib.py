@@ -49,6 +49,11 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p, _i64,
          _p, _size, _i32, _i32, _p],
     ),
+    "aac_decode_paged_noalloc": (
+        _c_int,
+        [_p, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p, _i64,
+         _i32, _i32, _p],
+    ),
     "aac_decode_append_paged": (
         _c_int,
         [_p, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _i32, _p, _i32, _p, _i32, _i32, _i32, _i32,

@@ -11,6 +11,9 @@ extern "C" const char* aac_strerror(int code) {
     case AAC_ERR_MISALIGNED: return "pointer or stride not aligned for vector access";
     case AAC_ERR_WORKSPACE: return "split-K workspace missing or too small";
     case AAC_ERR_SHAPE: return "inconsistent shape arguments";
+    case AAC_ERR_SCRATCH:
+      return "the split-K plan needs more than the library's static scratch "
+             "(AAC_DECODE_SCRATCH_BYTES); use the entry point with a workspace";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);

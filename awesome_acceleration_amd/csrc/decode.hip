@@ -49,6 +49,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <mutex>
 
 #include "aac_common.h"
 
@@ -658,6 +659,60 @@ extern "C" int aac_decode_paged(const void* q, int64_t q_seq_stride, const void*
                        max_blocks_per_seq, context_lens, 0, n_seqs, max_context_len, n_q_heads,
                        n_kv_heads, head_dim, scale, out, out_seq_stride, workspace,
                        workspace_bytes, partition_tokens, dtype, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ static scratch
+// Split-K scratch of aac_decode_paged_noalloc: one array per GPU, held until
+// the process ends.  In host code `scratch` names a host-side stand-in, not
+// device memory; the array's device address on each GPU comes from
+// hipGetSymbolAddress (looked up once per device, with that device current)
+// and only that address is handed to the kernels.
+static __device__ __align__(256) unsigned char scratch[AAC_DECODE_SCRATCH_BYTES];
+
+static int scratch_address(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return AAC_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return AAC_ERR_SCRATCH;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return AAC_OK;
+}
+
+extern "C" int aac_decode_paged_noalloc(const void* q, int64_t q_seq_stride, const void* k_cache,
+                                        const void* v_cache, int64_t num_blocks, int32_t block_size,
+                                        const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                        const int32_t* context_lens, int32_t n_seqs,
+                                        int32_t max_context_len, int32_t n_q_heads,
+                                        int32_t n_kv_heads, int32_t head_dim, float scale,
+                                        void* out, int64_t out_seq_stride,
+                                        int32_t partition_tokens, int32_t dtype, void* stream) {
+  // the plan is host arithmetic: a call it does not fit is rejected before
+  // the device is touched
+  const size_t need = aac_decode_workspace_bytes(n_seqs, n_q_heads, n_kv_heads, head_dim,
+                                                 block_size, max_blocks_per_seq, max_context_len,
+                                                 partition_tokens);
+  if (need > AAC_DECODE_SCRATCH_BYTES) return AAC_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (need) {
+    const int rc = scratch_address(&ws);
+    if (rc != AAC_OK) return rc;
+  }
+  return decode_common(q, q_seq_stride, k_cache, v_cache, num_blocks, block_size, block_tables,
+                       max_blocks_per_seq, context_lens, 0, n_seqs, max_context_len, n_q_heads,
+                       n_kv_heads, head_dim, scale, out, out_seq_stride, ws,
+                       need ? (size_t)AAC_DECODE_SCRATCH_BYTES : 0, partition_tokens, dtype,
+                       (hipStream_t)stream);
 }
 
 extern "C" int aac_decode_append_paged(const void* q, int64_t q_seq_stride, const void* k,

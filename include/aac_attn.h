@@ -5,7 +5,8 @@
  *
  * Conventions shared by every entry point
  *   - All tensor pointers are device pointers; every buffer is owned by the
- *     caller.  The library allocates no device memory.
+ *     caller.  The library allocates no device memory (aac_decode_paged_noalloc
+ *     uses one static device array instead of a workspace argument).
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *     Work is enqueued asynchronously; no entry point synchronises the host.
  *   - Strides are in ELEMENTS.  Within one token the [heads, head_dim] block
@@ -20,7 +21,8 @@
  *   - Return value: 0 on success, a negative AAC_ERR_* code for a rejected
  *     argument, or a positive hipError_t when a launch failed.  Nothing is
  *     thrown across the ABI; aac_strerror() gives the message.
- *   - Calls are stateless and reentrant.
+ *   - Calls are stateless and reentrant, except aac_decode_paged_noalloc,
+ *     whose calls share one scratch array per GPU.
  *
  * Reference interfaces replaced (reference paths are relative to the
  * yijichar/AWesome_ACceleration tree):
@@ -63,7 +65,8 @@ enum {
   AAC_ERR_UNSUPPORTED = -2,      /* dtype / head_dim / GQA group not built */
   AAC_ERR_MISALIGNED = -3,       /* pointer or stride breaks 16-B access  */
   AAC_ERR_WORKSPACE = -4,        /* split-K workspace too small           */
-  AAC_ERR_SHAPE = -5             /* inconsistent shape arguments          */
+  AAC_ERR_SHAPE = -5,            /* inconsistent shape arguments          */
+  AAC_ERR_SCRATCH = -6           /* plan exceeds the static decode scratch */
 };
 
 /* ABI revision of the loaded library (AAC_ABI_VERSION it was built with). */
@@ -177,6 +180,33 @@ int aac_decode_paged(const void* q, int64_t q_seq_stride, const void* k_cache, c
                      int32_t head_dim, float scale, void* out, int64_t out_seq_stride,
                      void* workspace, size_t workspace_bytes, int32_t partition_tokens,
                      int32_t dtype, void* stream);
+
+/* Bytes of the static split-K scratch aac_decode_paged_noalloc uses. */
+#define AAC_DECODE_SCRATCH_BYTES (64u << 20)
+
+/*
+ * aac_decode_paged without a workspace: the same kernels, plan and results,
+ * with the split-K partials in a static device array of
+ * AAC_DECODE_SCRATCH_BYTES that the library holds on each GPU it runs on
+ * until the process ends.  Allocates nothing (no hipMalloc, no library
+ * allocation): for callers that cannot allocate device memory -- code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it.  A plan
+ * whose workspace (aac_decode_workspace_bytes) exceeds the scratch returns
+ * AAC_ERR_SCRATCH before anything is enqueued.  Every call on a GPU shares
+ * that GPU's array (the device current on the calling thread), so calls
+ * that overlap on one GPU -- other streams or threads -- race and must be
+ * serialised by the caller; each call writes every scratch slot it reads, so
+ * nothing carries over between calls.
+ * No counterpart in the reference (whose flash_attn_with_kvcache allocates
+ * its split buffers itself): an extra for callers that cannot allocate.
+ */
+int aac_decode_paged_noalloc(const void* q, int64_t q_seq_stride, const void* k_cache,
+                             const void* v_cache, int64_t num_blocks, int32_t block_size,
+                             const int32_t* block_tables, int32_t max_blocks_per_seq,
+                             const int32_t* context_lens, int32_t n_seqs,
+                             int32_t max_context_len, int32_t n_q_heads, int32_t n_kv_heads,
+                             int32_t head_dim, float scale, void* out, int64_t out_seq_stride,
+                             int32_t partition_tokens, int32_t dtype, void* stream);
 
 /*
  * flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v, cache_seqlens,

@@ -79,7 +79,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_messages():
     L = _lib.lib()
     assert L.aac_abi_version() == _lib.ABI_VERSION
-    for code in (0, -1, -2, -3, -4, -5):
+    for code in (0, -1, -2, -3, -4, -5, -6):
         assert L.aac_strerror(code)
     assert b"unknown" in L.aac_strerror(-99)
 
