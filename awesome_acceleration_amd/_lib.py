@@ -36,8 +36,9 @@ SIGNATURES: dict[str, tuple] = {
     "aac_prefill_varlen": (
         _c_int,
         [_p, _p, _p, _i64, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
-         _p, _i64, _i32, _p],
+         _p, _i64, _p, _size, _i32, _p],
     ),
+    "aac_prefill_workspace_bytes": (_size, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "aac_prefill_varlen_store": (
         _c_int,
         [_p, _p, _p, _i64, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
@@ -79,7 +80,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, [_p, _p, _i64, _i64, _i32, _i64, _i32, _i32, _i32, _p, _i32, _i32, _i32, _p]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 AAC_DTYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 

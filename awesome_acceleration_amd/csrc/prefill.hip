@@ -77,6 +77,15 @@ struct Args {
   const int64_t* slots;
   int64_t num_rows;
   int32_t n_tok;  // k/v tokens the store covers
+  // Split keys (SPLIT): every item's key tiles are cut into up to n_split
+  // pieces, worked on by different workgroups; each piece leaves its
+  // unnormalised accumulators and (m, l) per lane in the workspace, and the
+  // last piece of an item to finish merges them (ws_cnt counts finished
+  // pieces and is reset to zero by the merging piece).
+  int32_t n_split;
+  float* ws_o;     // [item][piece][wave][16 float4][64 lanes]
+  float2* ws_ml;   // [item][piece][wave][64 lanes]: reference max, lane-partial sum
+  int32_t* ws_cnt; // [item]
 };
 
 template <bool F16> struct Mfma;
@@ -130,7 +139,7 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-template <int G, bool CAUSAL, bool F16, bool STORE>
+template <int G, bool CAUSAL, bool F16, bool STORE, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   constexpr int WH = G;                // head slots per workgroup (one head per wave)
   constexpr int WQ = kWaves / WH;      // 32-query slots per workgroup
@@ -142,6 +151,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   constexpr int kRingElems = STAGES * (BKV * KPITCH + D * BKV);
   static_assert(kWaves * 32 * OPITCH <= kRingElems, "output staging fits in the ring");
   __shared__ __attribute__((aligned(16))) u16 lds[kRingElems];
+  __shared__ int split_last;  // SPLIT: this workgroup's piece was its item's last
   auto Ks = [&](int st) { return lds + st * (BKV * KPITCH); };
   auto Vt = [&](int st) { return lds + STAGES * BKV * KPITCH + st * (D * BKV); };
 
@@ -192,17 +202,29 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   // heavy with light items, and skips the ranks a short segment lacks.
   struct Item {
     int h, s, qb, q_beg, Lq, k_beg, Lk;
+    int t0, t1;         // key tiles [t0, t1) of this piece (the whole range without SPLIT)
+    int id, piece, np;  // SPLIT: item number, piece, pieces of the item
   };
   const int n_hs = a.hkv * a.n_seqs;
-  const int n_items = n_hs * a.n_qblocks;
+  const int n_split = SPLIT ? a.n_split : 1;
+  const int per_rank = n_hs * n_split;  // work units of one q-block rank
+  const int n_items = per_rank * a.n_qblocks;
   const int P = gridDim.x, w = blockIdx.x;
   auto item_index = [&](int k) { return (k & 1) ? (k + 1) * P - 1 - w : k * P + w; };
-  auto seg_of = [&](int i) { return (i % n_hs) / a.hkv; };
+  auto seg_of = [&](int i) { return ((i % per_rank) % n_hs) / a.hkv; };
+  // keys visible to the whole workgroup (bottom-right causal alignment)
+  auto kv_end_of = [&](const Item& it) {
+    const int wg_qmax = min(it.qb * BQ + BQ, it.Lq) - 1;
+    return CAUSAL ? max(0, min(it.Lk, wg_qmax + 1 + it.Lk - it.Lq)) : it.Lk;
+  };
   // item i from its segment's bounds; false for a rank the segment lacks
   auto decode = [&](int i, int q0, int q1, int k0, int k1, Item& it) -> bool {
-    const int z = i / n_hs;
-    it.s = (i - z * n_hs) / a.hkv;
-    it.h = i - z * n_hs - it.s * a.hkv;
+    const int z = i / per_rank;
+    const int r = i - z * per_rank;
+    const int pc = SPLIT ? r / n_hs : 0;
+    const int hs = r - pc * n_hs;
+    it.s = hs / a.hkv;
+    it.h = hs - it.s * a.hkv;
     it.q_beg = q0;
     it.Lq = q1 - q0;
     it.k_beg = k0;
@@ -212,8 +234,21 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     it.Lk = min(k1 - k0, a.max_k);
     const int nqb = (it.Lq + BQ - 1) / BQ;
     it.qb = CAUSAL ? nqb - 1 - z : z;
-    return z < nqb;
+    if (z >= nqb) return false;
+    if constexpr (SPLIT) {
+      const int nt = (kv_end_of(it) + BKV - 1) / BKV;
+      it.id = z * n_hs + hs;
+      it.piece = pc;
+      it.np = min(n_split, max(nt, 1));
+      if (pc >= it.np) return false;  // a short item has fewer pieces
+      it.t0 = pc * nt / it.np;
+      it.t1 = (pc + 1) * nt / it.np;
+    }
+    return true;
   };
+  // key tiles [t_first, t_end) of an item's piece (all of them without SPLIT)
+  auto t_first = [&](const Item& it) { return SPLIT ? it.t0 : 0; };
+  auto t_end = [&](const Item& it, int kv_end) { return SPLIT ? it.t1 : (kv_end + BKV - 1) / BKV; };
   // first valid item of round k or later (k is left at its round)
   auto next_item = [&](int& k, Item& it) -> bool {
     for (; k * P < n_items; ++k) {
@@ -223,11 +258,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
       if (decode(i, a.cu_q[sg], a.cu_q[sg + 1], a.cu_k[sg], a.cu_k[sg + 1], it)) return true;
     }
     return false;
-  };
-  // keys visible to the whole workgroup (bottom-right causal alignment)
-  auto kv_end_of = [&](const Item& it) {
-    const int wg_qmax = min(it.qb * BQ + BQ, it.Lq) - 1;
-    return CAUSAL ? max(0, min(it.Lk, wg_qmax + 1 + it.Lk - it.Lq)) : it.Lk;
   };
   auto rsrc_of = [&](const Item& it, int kv_end) {
     const u16* base = (k_role ? a.k + (int64_t)it.k_beg * a.k_stride
@@ -395,13 +425,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   // (one copy at the loop top would merge the wait counts of the first item
   // with those of later items, which also have the previous item's output
   // stores outstanding).
-  auto prologue = [&](int nt_) {
+  auto prologue = [&](int t0, int t1) {
     f32x16 s0;
-    if (nt_ > 0) {
-      stage_write(0);
-      if (nt_ > 1) prefetch(1);
+    if (t1 > t0) {
+      stage_write(t0);
+      if (t1 > t0 + 1) prefetch(t0 + 1);
       __syncthreads();
-      s0 = scores(0);
+      s0 = scores(2 * t0);
     } else {
       // Q must be complete on this path too: Q left pending on any path into
       // the tile loop would make every tile wait for all vector loads,
@@ -415,8 +445,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   };
 
   load_q(cur);
-  prefetch(0);  // an empty resource (kv_end == 0) reads zeros
-  f32x16 sc = prologue((kv_end + BKV - 1) / BKV);
+  prefetch(t_first(cur));  // an empty resource (kv_end == 0) reads zeros
+  f32x16 sc = prologue(t_first(cur), t_end(cur, kv_end));
 
   for (;;) {
     // Segment bounds of the next round's item, loaded now so that they have
@@ -441,8 +471,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     const int w_end = w_qmin >= cur.Lq ? 0 : (CAUSAL ? max(0, min(cur.Lk, w_qmax + 1 + shift)) : cur.Lk);
     const int w_full = CAUSAL ? min(cur.Lk, w_qmin + 1 + shift) : cur.Lk;  // keys < w_full need no mask
     const int my_lim = CAUSAL ? min(cur.Lk, qi + 1 + shift) : cur.Lk;
-    const int nt = (kv_end + BKV - 1) / BKV;  // LDS tiles (workgroup-uniform)
-    const int nsub = (w_end + 31) / 32;       // 32-key sub-tiles this wave computes
+    const int t0 = t_first(cur), nt = t_end(cur, kv_end);  // LDS tiles [t0, nt) (workgroup-uniform)
+    const int nsub = (w_end + 31) / 32;  // 32-key sub-tiles this wave computes (of all keys)
 
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -458,7 +488,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     // which every wave has passed; the mid-tile barrier of iteration t makes
     // tile t+1 visible before the look-ahead of sub-tile 2t+1 reads it.  The
     // LDS writes thus overlap sub-tile 2t instead of preceding a barrier.
-    for (int t = 0; t < nt; ++t) {
+    for (int t = t0; t < nt; ++t) {
       if (t + 1 < nt) stage_write(t + 1);
       if (t + 2 < nt) prefetch(t + 2);
 #pragma unroll
@@ -489,7 +519,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
           // exceeds it by more than kRescale (log2 units), so p <= 2^kRescale
           // and the accumulators (normalised exactly at the end) are rescaled
           // rarely; on the first sub-tile they are still zero.
-          if (j == 0) {
+          if (j == 2 * t0) {
             m = vmax(mx, -1e30f);
           } else if (__any((mx - m) * a.scale_log2 > kRescale)) {
             const float mn = vmax(m, mx);
@@ -547,7 +577,108 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
       kv_end = kv_end_of(nxt);
       rs = rsrc_of(nxt, kv_end);
       load_q(nxt);
-      prefetch(0);
+      prefetch(t_first(nxt));
+    }
+
+    // ---- split keys: every piece of an item leaves its accumulators and
+    // (m, l) in the workspace, and the last piece of the item to finish
+    // merges the pieces in piece order -- the result does not depend on which
+    // piece finishes last -- and stores the output; the others store nothing.
+    // The workspace is written and read with agent-scope relaxed atomic
+    // accesses (coherent across XCDs without flushing the L2, which a fence
+    // would do), every piece waits for its writes to complete before it
+    // counts itself finished, and the merging piece resets the count to zero
+    // for the next call.  Nothing waits on another workgroup.
+    bool emit = true;
+    if (SPLIT && cur.np > 1) {
+      typedef unsigned long long u64;
+      const int64_t slot0 = (int64_t)cur.id * n_split;
+      // one buffer resource over this wave's accumulator blocks of every
+      // piece of the item: piece pc at pc * kPieceStride bytes, block (c, r)
+      // at (c*4 + r) * 1 KiB, lane at 16 B; accessed with the sc1 policy
+      // (coherent across XCDs, as the compiler's agent-scope atomics are)
+      constexpr int kPieceStride = kWaves * 16 * 64 * 16;
+      constexpr int kSc1 = 16;
+      const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<char*>(a.ws_o) + (slot0 * kWaves + wave) * (16 * 64 * 16), 0,
+          (n_split - 1) * kPieceStride + 16 * 64 * 16, 0x00020000);
+      auto pml = [&](int pc) {
+        return reinterpret_cast<u64*>(a.ws_ml + ((slot0 + pc) * kWaves + wave) * 64 + lane);
+      };
+      auto pack2 = [](float x, float y) {
+        return (u64)__float_as_uint(x) | ((u64)__float_as_uint(y) << 32);
+      };
+      {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = o[c][4 * r + i];
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
+                                                   lane * 16 + (c * 4 + r) * 1024,
+                                                   cur.piece * kPieceStride, kSc1);
+          }
+        __hip_atomic_store(pml(cur.piece), pack2(m, l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's writes have completed
+      __syncthreads();
+      if (tid == 0)
+        split_last = __hip_atomic_fetch_add(a.ws_cnt + cur.id, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) == cur.np - 1;
+      __syncthreads();
+      emit = split_last != 0;
+      if (emit) {
+        if (tid == 0) __hip_atomic_store(a.ws_cnt + cur.id, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float2 ml[4];
+        float mx = -1e30f;
+#pragma unroll
+        for (int pc = 0; pc < 4; ++pc) {
+          ml[pc] = make_float2(-1e30f, 0.f);
+          if (pc < cur.np) {
+            if (pc == cur.piece) {
+              ml[pc] = make_float2(m, l);
+            } else {
+              const u64 b = __hip_atomic_load(pml(pc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              ml[pc] = make_float2(__uint_as_float((u32)b), __uint_as_float((u32)(b >> 32)));
+            }
+          }
+          mx = vmax(mx, ml[pc].x);
+        }
+        float wt[4];
+        l = 0.f;
+#pragma unroll
+        for (int pc = 0; pc < 4; ++pc) {
+          wt[pc] = fast_exp2((ml[pc].x - mx) * a.scale_log2);
+          if (pc < cur.np) l = fmaf(ml[pc].y, wt[pc], l);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          f32x16 acc;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+          for (int pc = 0; pc < 4; ++pc) {
+            if (pc >= cur.np) continue;
+            if (pc == cur.piece) {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) acc[i] = fmaf(o[c][i], wt[pc], acc[i]);
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const f32x4 v = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, lane * 16 + (c * 4 + r) * 1024,
+                                                                 pc * kPieceStride, kSc1));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[4 * r + i] = fmaf(v[i], wt[pc], acc[4 * r + i]);
+              }
+            }
+          }
+          o[c] = acc;
+        }
+        m = mx;
+      }
     }
 
     // ---- epilogue: full row sum (partner lane holds the other 16 keys of
@@ -562,6 +693,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     const float inv = lt > 0.f ? __builtin_amdgcn_rcpf(lt) : 0.f;
     __syncthreads();  // every wave is done with the ring (including the discarded look-ahead)
     u16* ob = lds + wave * (32 * OPITCH);  // this wave's 32 rows x 128 dims
+    if (emit) {
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -590,6 +722,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
       for (int it = 0; it < 8; ++it)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val[it]), ors, voff, 4 * it * ostep, 0);
     }
+    }  // emit
     if (STORE) {
       KArgs* sa = sargs();
 #pragma unroll
@@ -602,30 +735,82 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     __syncthreads();
     cur = nxt;
     k = kn;
-    sc = prologue((kv_end + BKV - 1) / BKV);
+    sc = prologue(t_first(cur), t_end(cur, kv_end));
   }
   store_edges();
 }
 
-template <int G, bool CAUSAL, bool F16, bool STORE>
+template <int G, bool CAUSAL, bool F16, bool STORE, bool SPLIT>
 static void launch_t(Args a, int max_q, int n_cu, hipStream_t st) {
   constexpr int BQ = 32 * (kWaves / G);
   a.n_qblocks = (int)cdiv(max_q, BQ);
-  const int64_t n_items = (int64_t)a.hkv * a.n_seqs * a.n_qblocks;
+  const int64_t n_items = (int64_t)a.hkv * a.n_seqs * a.n_qblocks * (SPLIT ? a.n_split : 1);
   const int grid = (int)std::min<int64_t>(n_items, n_cu);  // persistent: one workgroup per CU
-  hipLaunchKernelGGL((prefill_kernel<G, CAUSAL, F16, STORE>), dim3(grid), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL((prefill_kernel<G, CAUSAL, F16, STORE, SPLIT>), dim3(grid), dim3(kThreads), 0, st,
+                     a);
 }
 
-template <bool CAUSAL, bool F16, bool STORE = false>
+template <bool CAUSAL, bool F16, bool STORE = false, bool SPLIT = false>
 static int launch_g(const Args& a, int g, int max_q, int n_cu, hipStream_t st) {
   switch (g) {
-    case 1: launch_t<1, CAUSAL, F16, STORE>(a, max_q, n_cu, st); break;
-    case 2: launch_t<2, CAUSAL, F16, STORE>(a, max_q, n_cu, st); break;
-    case 4: launch_t<4, CAUSAL, F16, STORE>(a, max_q, n_cu, st); break;
-    case 8: launch_t<8, CAUSAL, F16, STORE>(a, max_q, n_cu, st); break;
+    case 1: launch_t<1, CAUSAL, F16, STORE, SPLIT>(a, max_q, n_cu, st); break;
+    case 2: launch_t<2, CAUSAL, F16, STORE, SPLIT>(a, max_q, n_cu, st); break;
+    case 4: launch_t<4, CAUSAL, F16, STORE, SPLIT>(a, max_q, n_cu, st); break;
+    case 8: launch_t<8, CAUSAL, F16, STORE, SPLIT>(a, max_q, n_cu, st); break;
     default: return AAC_ERR_UNSUPPORTED;
   }
   return AAC_OK;
+}
+
+// ------------------------------------------------------------------ split plan
+// Two pieces per item when the items are too few for the CUs and long enough
+// that halving the heaviest one outweighs writing and merging the partial
+// results (128 KiB per piece).  Measured on MI355X (256 CUs, bf16, causal;
+// unsplit -> split, us): one 1024-token request 32.0 -> 27.4 (16/8 heads)
+// and 33.0 -> 28.2 (32/8), 2 x 1024 32.6 -> 28.8, 1 x 2048 58.5 -> 43.2,
+// 1 x 4096 111.9 -> 92.0; not split because it measured slower: 256 items
+// of at most 16 tiles (8 x 1024 at 8/4 heads 34.8 -> 43.0, 4 x 1024 at 16/8
+// 34.0 -> 43.3), items under 16 tiles (1 x 512 19.0 -> 19.4, 2 x 256
+// 12.3 -> 15.9); four pieces never beat two by more than noise.
+struct SplitPlan {
+  int32_t n_split;
+  int64_t n_items;  // items (without pieces): counters in the workspace
+  size_t ws_bytes;
+};
+constexpr int kMaxSplit = 2;
+constexpr size_t kPieceBytes = (size_t)kWaves * 64 * (64 * 4 + 8);  // accumulators + (m, l) per lane
+// The item counters sit in a region of fixed size at the start of every
+// workspace, so that no call's partial results ever land where a later call
+// (with more items) keeps its counters; calls with more items do not split.
+constexpr int64_t kMaxSplitItems = 4096;
+constexpr size_t kCntBytes = kMaxSplitItems * 4;
+
+static SplitPlan plan_split(int32_t n_seqs, int32_t max_q, int32_t max_k, int32_t hq, int32_t hkv,
+                            bool causal, int n_cu) {
+  SplitPlan p = {1, 0, 0};
+  if (n_seqs <= 0 || max_q <= 0 || max_k <= 0 || hkv <= 0 || hq % hkv || n_cu <= 0) return p;
+  const int g = hq / hkv;
+  if (g != 1 && g != 2 && g != 4 && g != 8) return p;
+  const int64_t BQ = 32 * (kWaves / g);
+  const int64_t nqb = cdiv(max_q, BQ);
+  const int64_t n_hs = (int64_t)hkv * n_seqs;
+  p.n_items = n_hs * nqb;
+  // plenty of items: nothing to gain (and the counters hold kMaxSplitItems)
+  if (p.n_items >= 4 * (int64_t)n_cu || p.n_items > kMaxSplitItems) return p;
+  auto tiles = [&](int64_t z) -> int64_t {  // key tiles of the q-block of rank z
+    if (!causal) return cdiv(max_k, BKV);
+    const int64_t qb = nqb - 1 - z;
+    const int64_t qmax = std::min<int64_t>((qb + 1) * BQ, max_q) - 1;
+    const int64_t ke = std::max<int64_t>(0, std::min<int64_t>(max_k, qmax + 1 + max_k - max_q));
+    return cdiv(ke, BKV);
+  };
+  const int64_t heavy = tiles(0);
+  const bool split = heavy >= 16 && (2 * p.n_items <= n_cu || (p.n_items <= n_cu && heavy >= 48));
+  if (!split) return p;
+  const int s = kMaxSplit;
+  p.n_split = s;
+  p.ws_bytes = kCntBytes + (size_t)p.n_items * s * kPieceBytes;
+  return p;
 }
 
 // Compute units of the current device (the persistent grid size), cached per
@@ -661,7 +846,8 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
                           int64_t out_tok_stride, int32_t dtype, hipStream_t stream,
                           bool launch, void* k_cache = nullptr, void* v_cache = nullptr,
                           int64_t num_cache_rows = 0, const int64_t* slot_mapping = nullptr,
-                          int32_t n_store = 0) {
+                          int32_t n_store = 0, void* workspace = nullptr,
+                          size_t workspace_bytes = 0) {
   if (dtype != AAC_DTYPE_BF16 && dtype != AAC_DTYPE_FP16) return AAC_ERR_UNSUPPORTED;
   if (head_dim != pf::D) return AAC_ERR_UNSUPPORTED;
   if (n_seqs < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || max_seqlen_q < 0 || max_seqlen_k < 0 ||
@@ -708,11 +894,29 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
   a.slots = slot_mapping;
   a.num_rows = num_cache_rows;
   a.n_tok = n_store;
+  a.n_split = 1;
+  a.ws_o = nullptr;
+  a.ws_ml = nullptr;
+  a.ws_cnt = nullptr;
   const bool f16 = dtype == AAC_DTYPE_FP16;
   int n_cu = 0;
   int rc = pf::device_cu_count(&n_cu);
   if (rc != AAC_OK) return rc;
-  if (n_store > 0)  // the store variant exists for causal attention only
+  // split keys when a workspace is given, the plan asks for it and the
+  // workspace holds it (otherwise the call runs unsplit)
+  pf::SplitPlan sp = {1, 0, 0};
+  if (n_store == 0 && workspace && (uintptr_t)workspace % 256 == 0)
+    sp = pf::plan_split(n_seqs, max_seqlen_q, max_seqlen_k, n_q_heads, n_kv_heads, causal != 0, n_cu);
+  if (sp.n_split > 1 && workspace_bytes >= sp.ws_bytes) {
+    a.n_split = sp.n_split;
+    a.ws_cnt = reinterpret_cast<int32_t*>(workspace);
+    a.ws_o = reinterpret_cast<float*>((char*)workspace + pf::kCntBytes);
+    a.ws_ml = reinterpret_cast<float2*>(a.ws_o + (size_t)sp.n_items * sp.n_split * pf::kWaves * 64 * 64);
+    rc = causal ? (f16 ? pf::launch_g<true, true, false, true>(a, g, max_seqlen_q, n_cu, stream)
+                       : pf::launch_g<true, false, false, true>(a, g, max_seqlen_q, n_cu, stream))
+                : (f16 ? pf::launch_g<false, true, false, true>(a, g, max_seqlen_q, n_cu, stream)
+                       : pf::launch_g<false, false, false, true>(a, g, max_seqlen_q, n_cu, stream));
+  } else if (n_store > 0)  // the store variant exists for causal attention only
     rc = f16 ? pf::launch_g<true, true, true>(a, g, max_seqlen_q, n_cu, stream)
              : pf::launch_g<true, false, true>(a, g, max_seqlen_q, n_cu, stream);
   else if (causal)
@@ -730,17 +934,29 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
 
 using namespace aac;
 
+extern "C" size_t aac_prefill_workspace_bytes(int32_t n_seqs, int32_t max_seqlen_q,
+                                              int32_t max_seqlen_k, int32_t n_q_heads,
+                                              int32_t n_kv_heads, int32_t head_dim,
+                                              int32_t causal) {
+  if (head_dim != pf::D) return 0;
+  int n_cu = 0;
+  if (pf::device_cu_count(&n_cu) != AAC_OK) return 0;
+  return pf::plan_split(n_seqs, max_seqlen_q, max_seqlen_k, n_q_heads, n_kv_heads, causal != 0, n_cu)
+      .ws_bytes;
+}
+
 extern "C" int aac_prefill_varlen(const void* q, const void* k, const void* v, int64_t q_tok_stride,
                                   int64_t k_tok_stride, int64_t v_tok_stride,
                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                   int32_t n_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
                                   int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
                                   float scale, int32_t causal, void* out, int64_t out_tok_stride,
-                                  int32_t dtype, void* stream) {
+                                  void* workspace, size_t workspace_bytes, int32_t dtype,
+                                  void* stream) {
   return prefill_common(q, k, v, q_tok_stride, k_tok_stride, v_tok_stride, cu_seqlens_q,
                         cu_seqlens_k, n_seqs, max_seqlen_q, max_seqlen_k, n_q_heads, n_kv_heads,
                         head_dim, scale, causal, out, out_tok_stride, dtype, (hipStream_t)stream,
-                        true);
+                        true, nullptr, nullptr, 0, nullptr, 0, workspace, workspace_bytes);
 }
 
 extern "C" int aac_kv_store(const void* k, const void* v, int64_t k_tok_stride,

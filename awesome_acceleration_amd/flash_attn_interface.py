@@ -105,6 +105,25 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
         return buf
 
 
+_pf_ws: dict[int, torch.Tensor] = {}
+
+
+def _prefill_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Per-device workspace of the split-key prefill: zero-filled when it is
+    allocated (its leading per-item counters must start at zero; every call
+    leaves them at zero), grown on demand, and never shared with the decode
+    workspace.  Outgrown buffers stay alive (a captured graph may hold them)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        buf = _pf_ws.get(idx)
+        if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                _ws_retired.append(buf)
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _pf_ws[idx] = buf
+        return buf
+
+
 # ---------------------------------------------------------------- KV store
 def check_mode() -> bool:
     """Whether ``AAC_CHECK`` is set: the stores then validate slot_mapping as
@@ -204,11 +223,18 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
         return out
     if k.shape[0] == 0:  # no key anywhere: every row sees none
         return out.zero_()
-    rc = _lib.lib().aac_prefill_varlen(
+    L = _lib.lib()
+    n_seqs = cu_seqlens_q.shape[0] - 1
+    ws_bytes = L.aac_prefill_workspace_bytes(n_seqs, int(max_seqlen_q), int(max_seqlen_k),
+                                             q.shape[1], k.shape[1], q.shape[2],
+                                             int(bool(causal)))
+    ws = _prefill_workspace(ws_bytes, q.device) if ws_bytes else None
+    rc = L.aac_prefill_varlen(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), qs, ks, vs, cu_seqlens_q.data_ptr(),
-        cu_seqlens_k.data_ptr(), cu_seqlens_q.shape[0] - 1, int(max_seqlen_q), int(max_seqlen_k),
+        cu_seqlens_k.data_ptr(), n_seqs, int(max_seqlen_q), int(max_seqlen_k),
         q.shape[1], k.shape[1], q.shape[2], scale, int(bool(causal)), out.data_ptr(),
-        out.stride(0), _dtype_code(q), _stream(q))
+        out.stride(0), ws.data_ptr() if ws is not None else None, ws_bytes, _dtype_code(q),
+        _stream(q))
     _lib.check(rc, "aac_prefill_varlen")
     return out
 

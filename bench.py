@@ -394,7 +394,38 @@ def bench_prefill(torch, fai, paged, dev, args, hq=16, hkv=8):
     warm(torch, [step, attend], args.warmup_seconds)
     t_step = launch_avg(torch, step, args.steps)
     t_att = launch_avg(torch, attend, args.steps)
-    return dict(t_step=t_step, t_attend=t_att, flops=flops, tflops=flops / t_att / 1e12)
+    return dict(t_step=t_step, t_attend=t_att, flops=flops, tflops=flops / t_att / 1e12,
+                sdpa=torch_sdpa_reference(torch, dev, args, nseq, L, hq, hkv, causal, flops))
+
+
+def torch_sdpa_reference(torch, dev, args, nseq, L, hq, hkv, causal, flops):
+    """The platform library's own flash attention on the same shape, for
+    reference: torch's scaled_dot_product_attention restricted to its flash
+    backend (no fallback to the math path), batch-padded [nseq, hq, L, 128]
+    bf16 with the KV heads repeated (equal lengths, so the same work as the
+    varlen call).  None when the backend is unavailable."""
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        g = torch.Generator(device=dev).manual_seed(args.seed)
+        q = torch.randn((nseq, hq, L, 128), generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn((nseq, hkv, L, 128), generator=g, device=dev).to(torch.bfloat16)
+        k = k.repeat_interleave(hq // hkv, dim=1).contiguous()
+        v = torch.randn_like(k)
+
+        def f():
+            with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+                return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+        for _ in range(3):
+            f()
+        warm(torch, [f], min(args.warmup_seconds, 0.5))
+        t = launch_avg(torch, f, max(5, args.steps // 2))
+        del q, k, v
+        return {"what": "torch scaled_dot_product_attention, flash backend only, same shape "
+                        "batch-padded, KV heads repeated", "us": round(t * 1e6, 2),
+                "achieved": round(flops / t / 1e12, 2), "unit": "TFLOP/s"}
+    except Exception as e:  # backend missing on this build: report, do not fail the bench
+        return {"what": "torch SDPA flash backend", "unavailable": f"{type(e).__name__}: {e}"[:200]}
 
 
 def bench_prefill_long(torch, fai, dev, args, nseq=8, L=8192, hq=16, hkv=8):
@@ -833,6 +864,7 @@ def main():
                          "traffic_with_store": measured_traffic(TRAFFIC_PREFILL,
                                                                 "traffic_bytes_per_launch_store"),
                          "traffic_source": TRAFFIC_PREFILL},
+            "torch_sdpa_flash": pf.get("sdpa"),
         }
     if "decode_long" in res:
         line["decode_long"] = res["decode_long"]

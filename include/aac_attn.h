@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define AAC_ABI_VERSION 1
+#define AAC_ABI_VERSION 2
 
 /* element types */
 enum {
@@ -118,6 +118,16 @@ int aac_kv_append_paged(const void* k, const void* v, int64_t k_tok_stride, int6
  *   out [Nq, n_q_heads, head_dim]  token stride out_tok_stride
  * max_seqlen_q / max_seqlen_k bound the segment lengths (as in FA2; they size
  * the launch grid).  Built for dtype BF16/FP16, head_dim 128, group 1/2/4/8.
+ * With too few (or too uneven) work items for the GPU -- one or a few
+ * requests, or a tensor-parallel rank's share of the heads -- the key range
+ * of each item is split over up to 4 workgroups whose partial results are
+ * merged by a log-sum-exp combine (in a fixed order: results are the same
+ * on every run).  The split needs `workspace` of
+ * aac_prefill_workspace_bytes(...) bytes, 256-byte aligned, ZERO-FILLED
+ * ONCE when it is allocated: its first 16 KiB are per-item counters that
+ * every call leaves at zero again, the rest partial results (do not share
+ * it with other data or with calls that overlap on another stream).
+ * workspace NULL, too small or misaligned: the call runs without a split.
  * Replaces flash_attn_varlen_func (llm.py:178-184).
  */
 int aac_prefill_varlen(const void* q, const void* k, const void* v, int64_t q_tok_stride,
@@ -125,7 +135,16 @@ int aac_prefill_varlen(const void* q, const void* k, const void* v, int64_t q_to
                        const int32_t* cu_seqlens_k, int32_t n_seqs, int32_t max_seqlen_q,
                        int32_t max_seqlen_k, int32_t n_q_heads, int32_t n_kv_heads,
                        int32_t head_dim, float scale, int32_t causal, void* out,
-                       int64_t out_tok_stride, int32_t dtype, void* stream);
+                       int64_t out_tok_stride, void* workspace, size_t workspace_bytes,
+                       int32_t dtype, void* stream);
+
+/*
+ * Workspace bytes aac_prefill_varlen would use to split this shape's key
+ * ranges on the current device (0: the plan does not split).
+ */
+size_t aac_prefill_workspace_bytes(int32_t n_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                   int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                                   int32_t causal);
 
 /*
  * The result of aac_kv_store(k, v -> caches via slot_mapping) followed by
@@ -135,7 +154,8 @@ int aac_prefill_varlen(const void* q, const void* k, const void* v, int64_t q_to
  * every one of them is stored, also tokens outside all segments.  Causal
  * self-attention (cu_seqlens_q == cu_seqlens_k as pointers, equal max_seqlen)
  * runs as one kernel that stores each q-block's K/V rows after attending to
- * them; other calls launch the store, then the attention.
+ * them; other calls launch the store, then the attention.  This call never
+ * splits key ranges (no workspace).
  */
 int aac_prefill_varlen_store(const void* q, const void* k, const void* v, int64_t q_tok_stride,
                              int64_t k_tok_stride, int64_t v_tok_stride,

@@ -100,7 +100,7 @@ def test_host_side_argument_rejection():
                               None, 0, None, 0, 0, 0, None) == -5
     # prefill: fp32 is not supported on the MFMA path
     assert L.aac_prefill_varlen(None, None, None, 0, 0, 0, None, None, 1, 1, 1, 16, 8, 128,
-                                1.0, 1, None, 0, 2, None) == -2
+                                1.0, 1, None, 0, None, 0, 2, None) == -2
     # KV export/import: unknown dtype, a table too short for the length, nothing to
     # move, null pointers with work to do, a misaligned buffer
     ex, im = L.aac_kv_export_paged, L.aac_kv_import_paged

@@ -255,3 +255,73 @@ def test_store_in_the_attention_kernel_covers_every_token(gpu, hq, hkv, dtype, c
             ref = oracle.varlen_attention(f64(q), f64(k), f64(v), cu_np, causal=causal)[a:b]
             absv = oracle.varlen_attention(f64(q), f64(k), np.abs(f64(v)), cu_np, causal=causal)[a:b]
             check_attention(out[a:b], ref, what="attention beside the store", absv=absv)
+
+
+def _unsplit(q, k, v, cq, ck, Lq, Lk, causal, scale):
+    """aac_prefill_varlen without a workspace: the same kernel, never split."""
+    from awesome_acceleration_amd import _lib
+    out = torch.empty_like(q)
+    rc = _lib.lib().aac_prefill_varlen(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), v.stride(0),
+        cq.data_ptr(), ck.data_ptr(), cq.shape[0] - 1, Lq, Lk, q.shape[1], k.shape[1], 128, scale,
+        int(causal), out.data_ptr(), out.stride(0), None, 0, _lib.AAC_DTYPE[q.dtype],
+        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.lib().aac_strerror(rc)
+    return out
+
+
+@pytest.mark.parametrize("lens_q,lens_k,hq,hkv,causal,dtype", [
+    ([1024], [1024], 16, 8, True, torch.bfloat16),        # one request: 64 items for 256 CUs
+    ([2048] * 2, [2048] * 2, 8, 4, True, torch.bfloat16),  # a TP=2 rank's heads, 2 requests
+    ([300, 1000], [300, 1000], 16, 8, True, torch.bfloat16),
+    ([512], [2048], 32, 8, False, torch.bfloat16),          # non-causal, Lq != Lk
+    ([1500], [1500], 8, 8, True, torch.float16),
+    ([200, 5, 600], [260, 5, 1200], 16, 4, True, torch.bfloat16),  # Lq < Lk, bottom-right
+])
+def test_split_keys_match_unsplit_and_oracle(gpu, lens_q, lens_k, hq, hkv, causal, dtype):
+    """Few work items: the key range of every item is split over several
+    workgroups and merged (log-sum-exp) by the last piece to finish.  The
+    result matches the oracle to the same bound as the unsplit kernel, is
+    close to it, and is the same on every call (fixed merge order; the
+    per-item counters are back at zero after each call)."""
+    print(f"case: split prefill q={lens_q} k={lens_k} {hq}/{hkv} causal={causal} {dtype}",
+          flush=True)
+    from awesome_acceleration_amd import _lib
+    q, k, v, cq, ck = _ragged(lens_q, lens_k, hq, hkv, dtype, gpu, seed=31)
+    Lq, Lk = max(lens_q), max(lens_k)
+    ws = _lib.lib().aac_prefill_workspace_bytes(len(lens_q), Lq, Lk, hq, hkv, 128, int(causal))
+    assert ws > 0, "the plan should split this shape"
+    scale = 128 ** -0.5
+    outs = [fai.flash_attn_varlen_func(q, k, v, cq, ck, Lq, Lk, causal=causal) for _ in range(3)]
+    base = _unsplit(q, k, v, cq, ck, Lq, Lk, causal, scale)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    cq_np, ck_np = cq.cpu().numpy(), ck.cpu().numpy()
+    ref = oracle.varlen_attention(f64(q), f64(k), f64(v), cq_np, ck_np, scale=scale, causal=causal)
+    absv = oracle.varlen_attention(f64(q), f64(k), np.abs(f64(v)), cq_np, ck_np, scale=scale,
+                                   causal=causal)
+    check_attention(outs[0], ref, what="split", absv=absv)
+    check_attention(base, ref, what="unsplit", absv=absv)
+    assert float((outs[0].float() - base.float()).abs().max()) <= 2 ** -6
+
+
+def test_split_workspace_reused_by_a_call_with_more_items(gpu):
+    """Regression: a split call with few items leaves partial results in the
+    shared workspace; a later split call with more items keeps its item
+    counters in the same fixed region at the start, which no partial result
+    ever overwrites, so every row of the later call is written."""
+    print("case: split workspace reuse, few then many items", flush=True)
+    from awesome_acceleration_amd import _lib
+    small = _ragged([1024], [1024], 16, 8, torch.bfloat16, gpu, seed=41)      # 64 items, split
+    big = _ragged([2048] * 2, [2048] * 2, 8, 4, torch.bfloat16, gpu, seed=42)  # 128 items, split
+    assert _lib.lib().aac_prefill_workspace_bytes(1, 1024, 1024, 16, 8, 128, 1) > 0
+    assert _lib.lib().aac_prefill_workspace_bytes(2, 2048, 2048, 8, 4, 128, 1) > 0
+    for (q, k, v, cq, ck) in (small, big, small, big):
+        L = int((cq[1:] - cq[:-1]).max())
+        out = torch.full_like(q, float("nan"))
+        out.copy_(fai.flash_attn_varlen_func(q, k, v, cq, ck, L, L, causal=True))
+        base = _unsplit(q, k, v, cq, ck, L, L, True, 128 ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all()
+        assert float((out.float() - base.float()).abs().max()) <= 2 ** -6
