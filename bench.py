@@ -29,19 +29,32 @@ Also reported on the same line:
                 8 TB/s; the host-inclusive request export (PCIe) beside it;
   prefill       varlen causal prefill, 8 x 1024 tokens, 16/8 heads, bf16, with
                 the paged store in the same call, as TFLOP/s against the
-                2.5 PFLOP/s dense bf16 MFMA peak (roofline of that kernel);
+                2.5 PFLOP/s dense bf16 MFMA peak (roofline of that kernel),
+                and torch's own flash attention (SDPA, flash backend) on the
+                same shape for reference;
+  prefill_one_request  one 2048-token request: too few work items for the
+                CUs, so each item's key range is split over two workgroups
+                (the same call unsplit beside it);
   prefill_long  the same kernel on 8 x 8192 causal tokens: its steady-state
                 rate, where per-item start and epilogue costs are small;
+  decode_fp32_small  the fp32 decode of the CPU-runnable case (4 seqs,
+                contexts 17/64/200/511) on the GPU, with its host figure;
   e2e           random-init Qwen3-0.6B, 256 requests x 1024 input / 1024
                 output tokens under the continuous-batching engine: output
                 tok/s (generated tokens / wall clock from submit to the last
                 token) and total tok/s (prompt + generated), as
                 benchmark_tp.py:93-99 defines them;
-  cpu_baseline  the numpy oracle on a bounded sample of the decode workload,
-                single-threaded on the host cores; e2e.cpu_baseline is the
-                end-to-end decode step on the host (one decoder layer for all
-                256 sequences in fp32 torch on up to 16 host threads, times 28
-                layers, plus lm_head) as output tok/s beside the GPU's.
+  cpu_baseline  the reference's semantics in fp32 torch on the host cores
+                (oracle/torch_path.py: index_copy_ store + attention; threads
+                = the cores this process may use, capped by OMP_NUM_THREADS),
+                3 warm-ups then the median of 5: the decode step of the
+                headline workload here, the prefill and long-context decode
+                legs' own figures inside them; oracle_1core is the numpy
+                float64 oracle on one core.  e2e.cpu_baseline is a complete
+                small generation run on the host (oracle/qwen3_ref.py, 8
+                requests x 128 in / 32 out); e2e.cpu_decode_step_extrapolated
+                one decoder layer's decode step for all 256 sequences times
+                28 layers plus lm_head.
 
 `python bench.py --gpus N --steps K --warmup W`; only N=1 is supported (one
 GPU), N>1 exits with a message.  Before its timed region every leg runs W
@@ -108,7 +121,7 @@ def parse():
     p.add_argument("--e2e-out", type=int, default=1024)
     p.add_argument("--only", choices=["decode", "decode_fp32_small", "decode_slot", "decode_long",
                                       "tp2_rank", "kv_transfer",
-                                      "prefill", "prefill_long", "e2e"],
+                                      "prefill", "prefill_one", "prefill_long", "e2e"],
                    default=None,
                    help="run one leg only (for profiling)")
     return p.parse_args()
@@ -458,6 +471,46 @@ def bench_prefill_long(torch, fai, dev, args, nseq=8, L=8192, hq=16, hkv=8):
     }
 
 
+def bench_prefill_one_request(torch, fai, dev, args, L=2048, hq=16, hkv=8):
+    """One 2048-token request (16/8 heads, causal): 128 work items for 256
+    CUs, so each item's key range is split over two workgroups and merged;
+    the same call without the split (no workspace) beside it."""
+    from awesome_acceleration_amd import _lib
+    d = 128
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn((L, hq, d), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((L, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((L, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    cu = torch.tensor([0, L], dtype=torch.int32, device=dev)
+    flops = 4 * hq * d * (L * (L + 1) // 2)
+    out = torch.empty_like(q)
+    lib, st = _lib.lib(), torch.cuda.current_stream().cuda_stream
+
+    def split():
+        return fai.flash_attn_varlen_func(q, k, v, cu, cu, L, L, causal=True)
+
+    def unsplit():
+        lib.aac_prefill_varlen(q.data_ptr(), k.data_ptr(), v.data_ptr(), hq * d, hkv * d, hkv * d,
+                               cu.data_ptr(), cu.data_ptr(), 1, L, L, hq, hkv, d, d ** -0.5, 1,
+                               out.data_ptr(), hq * d, None, 0, 0, st)
+
+    for _ in range(3):
+        split()
+        unsplit()
+    warm(torch, [split, unsplit], min(args.warmup_seconds, 0.5))
+    t = launch_avg(torch, split, args.steps)
+    t0 = launch_avg(torch, unsplit, args.steps)
+    ws = lib.aac_prefill_workspace_bytes(1, L, L, hq, hkv, d, 1)
+    return {"workload": f"varlen causal prefill of one {L}-token request, {hq}/{hkv} heads, "
+                        "head_dim 128, bf16: key ranges split over two workgroups and merged",
+            "us_attend": round(t * 1e6, 2), "us_unsplit": round(t0 * 1e6, 2),
+            "workspace_bytes": int(ws),
+            "roofline": {"bound": "mfma", "achieved": round(flops / t / 1e12, 2),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4),
+                         "flops_per_launch": flops}}
+
+
 # ----------------------------------------------------------------------------
 # end to end: random-init Qwen3-0.6B under the continuous-batching engine
 # ----------------------------------------------------------------------------
@@ -798,6 +851,8 @@ def main():
         res["kv_transfer"] = bench_kv_transfer(torch, dev, args)
     if args.only in (None, "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, fai, paged, dev, args)
+    if args.only in (None, "prefill_one") and not args.no_prefill:
+        res["prefill_one_request"] = bench_prefill_one_request(torch, fai, dev, args)
     if args.only in (None, "prefill_long") and not args.no_prefill_long:
         res["prefill_long"] = bench_prefill_long(torch, fai, dev, args)
         torch.cuda.empty_cache()
@@ -872,6 +927,8 @@ def main():
         line["decode_slot"] = res["decode_slot"]
     if "prefill_long" in res:
         line["prefill_long"] = res["prefill_long"]
+    if "prefill_one_request" in res:
+        line["prefill_one_request"] = res["prefill_one_request"]
     if "tp2_rank" in res:
         line["tp2_rank"] = res["tp2_rank"]
     if "kv_transfer" in res:
