@@ -269,3 +269,39 @@ def test_decode_many_sequences_dispatch_order(gpu, B):
     absv = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), 0.1, abs_v=True)
     check_attention(out, np.stack([ref[b] for b in range(B)]), what=f"B={B}",
                     absv=np.stack([absv[b] for b in range(B)]))
+
+
+def test_decode_long_context_all_sequences_vs_torch_fp32(gpu):
+    """Config 4 at full size: all 64 sequences (32 query / 8 KV heads,
+    context U[16384, 32768], block 256, split-K + log-sum-exp reduction)
+    against a plain fp32 torch reference of the same op on the GPU
+    (softmax(scale q K^T) V per sequence, KV heads repeated for GQA, the
+    probabilities' bf16 rounding bounded per element as in check_attention)."""
+    print("case: decode long context gqa4, all 64 sequences vs fp32 torch", flush=True)
+    B, hq, hkv, bs = 64, 32, 8, 256
+    rs = np.random.RandomState(1)
+    ctx = rs.randint(16384, 32769, B).astype(np.int32)
+    q, kc, vc, _, _, bt = _random_paged(B, hq, hkv, ctx, bs, 1, gpu, extra_blocks=0)
+    scale = 128 ** -0.5
+    out = fai.decode_paged(q, kc, vc, torch.from_numpy(bt).to(gpu), torch.from_numpy(ctx).to(gpu),
+                           scale, max_context_len=32768)
+    torch.cuda.synchronize()
+    g = hq // hkv
+    worst = 0.0
+    for b in range(B):
+        n = int(ctx[b])
+        blocks = torch.from_numpy(bt[b, :-(-n // bs)].astype(np.int64)).to(gpu)
+        k = kc[blocks].reshape(-1, hkv, 128)[:n].float()            # [n, hkv, D]
+        v = vc[blocks].reshape(-1, hkv, 128)[:n].float()
+        qh = q[b].float().view(hkv, g, 128)                         # [hkv, g, D]
+        s = torch.matmul(qh, k.permute(1, 2, 0).contiguous()) * scale   # [hkv, g, n]
+        p = torch.softmax(s, dim=-1)
+        vt = v.permute(1, 0, 2).contiguous()                        # [hkv, n, D]
+        ref = torch.matmul(p, vt).reshape(hq, 128)
+        absv = torch.matmul(p, vt.abs()).reshape(hq, 128)
+        err = (out[b].float() - ref).abs()
+        lim = 2.0 ** -8 * (ref.abs() + absv) + 1e-3
+        assert bool((err <= lim).all()), f"sequence {b}: {float((err - lim).max()):.3e} over the bound"
+        worst = max(worst, float(err.max()))
+    assert worst <= 2e-2
+    print(f"max-abs error over all 64 sequences {worst:.3e}", flush=True)
