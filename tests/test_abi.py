@@ -125,3 +125,23 @@ def test_workspace_sizing():
 def test_check_raises_runtime_error():
     with pytest.raises(RuntimeError, match="invalid argument"):
         _lib.check(-1, "probe")
+
+
+def test_header_compiles_as_c_and_links(tmp_path):
+    """A plain C99 program includes include/aac_attn.h, links the library and
+    calls its host-side paths (tests/c_abi_check.c): the boundary is usable
+    from C, not only through ctypes."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    exe = tmp_path / "c_abi_check"
+    src = Path(__file__).resolve().parent / "c_abi_check.c"
+    libdir = LIB_PATH.parent
+    r = subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", str(HEADER.parent), str(src),
+                        "-o", str(exe), f"-L{libdir}", "-laac_attn", f"-Wl,-rpath,{libdir}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout + r.stderr
