@@ -112,7 +112,9 @@ def _prefill_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     """Per-device workspace of the split-key prefill: zero-filled when it is
     allocated (its leading per-item counters must start at zero; every call
     leaves them at zero), grown on demand, and never shared with the decode
-    workspace.  Outgrown buffers stay alive (a captured graph may hold them)."""
+    workspace.  Outgrown buffers stay alive (a captured graph may hold them).
+    Like the decode workspace it is one buffer per device: prefills that
+    overlap on different streams of one device would share its counters."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     with _ws_lock:
         buf = _pf_ws.get(idx)
