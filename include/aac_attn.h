@@ -117,12 +117,15 @@ int aac_kv_append_paged(const void* k, const void* v, int64_t k_tok_stride, int6
  *   k,v [Nk, n_kv_heads, head_dim] token strides k_tok_stride / v_tok_stride
  *   out [Nq, n_q_heads, head_dim]  token stride out_tok_stride
  * max_seqlen_q / max_seqlen_k bound the segment lengths (as in FA2; they size
- * the launch grid).  Built for dtype BF16/FP16, head_dim 128, group 1/2/4/8.
- * With too few (or too uneven) work items for the GPU -- one or a few
- * requests, or a tensor-parallel rank's share of the heads -- the key range
- * of each item is split over up to 4 workgroups whose partial results are
- * merged by a log-sum-exp combine (in a fixed order: results are the same
- * on every run).  The split needs `workspace` of
+ * the launch grid).  A caller that understates them gets what FA2 gives:
+ * a segment longer than max_seqlen_q has rows the grid does not cover, left
+ * unwritten (here the segment's first rows, since causal q-blocks are
+ * numbered from its end), and only its first max_seqlen_k keys are
+ * attended; no access leaves the segment's rows.  Built for dtype
+ * BF16/FP16, head_dim 128, group 1/2/4/8.  With too few work items for the
+ * GPU -- one or a few long requests -- the key range of each item is split
+ * over two workgroups whose partial results are merged by a log-sum-exp
+ * combine (in a fixed order: results are the same on every run).  The split needs `workspace` of
  * aac_prefill_workspace_bytes(...) bytes, 256-byte aligned, ZERO-FILLED
  * ONCE when it is allocated: its first 16 KiB are per-item counters that
  * every call leaves at zero again, the rest partial results (do not share
