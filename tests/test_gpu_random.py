@@ -3,6 +3,9 @@ the targeted tests vary one at a time: segment lengths (empty, Lq != Lk),
 token strides, GQA group, dtype, softmax scale, causal or not (prefill);
 batch, context length, block size (power of two or not), partitioning,
 dtype, append (decode); slot mappings with padding and repeated rounds (KV store).
+Long segments (split key ranges) and the store inside the attention kernel
+are checked against a float64 torch restatement on the GPU, at shapes the
+numpy oracle would take minutes over.
 
 Every case prints its parameters before the GPU call; the seeds are fixed, so
 a failure names a reproducible case."""
@@ -11,6 +14,7 @@ import pytest
 import torch
 
 import oracle
+from awesome_acceleration_amd import _lib
 from awesome_acceleration_amd import flash_attn_interface as fai
 from gpu_util import bytes_of, check_attention, f64, np_of
 
@@ -149,3 +153,125 @@ def test_kv_store_random(gpu, seed):
         oracle.kv_store(ve, np_of(v), sm)
         assert _same_bytes(kc, ke), f"k cache round {rnd}"
         assert _same_bytes(vc, ve), f"v cache round {rnd}"
+
+
+def _torch_reference(q, k, v, lq, lk, scale, causal):
+    """Float64 restatement on the GPU of the oracle's varlen attention (the
+    same bottom-right causal mask and GQA head mapping), for shapes the numpy
+    oracle would take minutes over; returns the attention and the same with
+    |V| (the rounding-bound term of check_attention)."""
+    G = q.shape[1] // k.shape[1]
+    outs, absvs = [], []
+    oq = ok = 0
+    for a, b in zip(lq, lk):
+        Q = q[oq:oq + a].double().permute(1, 0, 2).contiguous()
+        K = k[ok:ok + b].double().repeat_interleave(G, dim=1).permute(1, 2, 0).contiguous()
+        V = v[ok:ok + b].double().repeat_interleave(G, dim=1).permute(1, 0, 2).contiguous()
+        s = torch.bmm(Q, K) * scale
+        if causal:
+            i = torch.arange(a, device=q.device).view(a, 1)
+            j = torch.arange(b, device=q.device).view(1, b)
+            s = s.masked_fill(j > i + (b - a), float("-inf"))
+        p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)  # no visible key: zeros
+        outs.append(torch.bmm(p, V).permute(1, 0, 2))
+        absvs.append(torch.bmm(p, V.abs()).permute(1, 0, 2))
+        oq += a
+        ok += b
+    return torch.cat(outs).cpu().numpy(), torch.cat(absvs).cpu().numpy()
+
+
+def _unsplit(q, k, v, cq, ck, mq, mk, scale, causal):
+    """aac_prefill_varlen without a workspace: the key ranges are never split."""
+    out = torch.empty_like(q)
+    rc = _lib.lib().aac_prefill_varlen(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), v.stride(0),
+        cq.data_ptr(), ck.data_ptr(), cq.shape[0] - 1, mq, mk, q.shape[1], k.shape[1], 128, scale,
+        int(causal), out.data_ptr(), out.stride(0), None, 0, 0 if q.dtype == torch.bfloat16 else 1,
+        torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "aac_prefill_varlen")
+    return out
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_split_random(gpu, seed):
+    """Few long segments (the shapes whose key ranges are split over two
+    workgroups when the plan asks for it): the split result equals itself on a
+    second call and both it and the unsplit kernel meet the parity bound."""
+    rs = np.random.RandomState(7000 + seed)
+    hkv = int(rs.choice([1, 2, 4, 8]))
+    hq = hkv * int(rs.choice([1, 2, 4]))
+    nseg = int(rs.randint(1, 4))
+    lq = [int(x) for x in rs.randint(700, 4200, nseg)]
+    if nseg > 1 and rs.randint(3) == 0:
+        lq[int(rs.randint(nseg))] = int(rs.choice([0, 1, 63, 300]))
+    causal = bool(rs.randint(3))
+    lk = [x + int(rs.randint(0, 300)) if causal else int(rs.randint(1, 4200)) for x in lq]
+    dtype = _DT[int(rs.randint(2))]
+    scale = float(rs.uniform(0.05, 0.2))
+    mq, mk = max(lq), max(lk)
+    ws = _lib.lib().aac_prefill_workspace_bytes(nseg, mq, mk, hq, hkv, 128, int(causal))
+    print(f"case: split prefill seed={seed} hq={hq} hkv={hkv} lq={lq} lk={lk} causal={causal} "
+          f"{dtype} workspace={ws}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    q = torch.randn((sum(lq), hq, 128), generator=g, device=gpu).to(dtype)
+    k = torch.randn((sum(lk), hkv, 128), generator=g, device=gpu).to(dtype)
+    v = torch.randn((sum(lk), hkv, 128), generator=g, device=gpu).to(dtype)
+    cq = torch.tensor(np.concatenate([[0], np.cumsum(lq)]), dtype=torch.int32, device=gpu)
+    ck = torch.tensor(np.concatenate([[0], np.cumsum(lk)]), dtype=torch.int32, device=gpu)
+    out = fai.flash_attn_varlen_func(q, k, v, cq, ck, mq, mk, softmax_scale=scale, causal=causal)
+    again = fai.flash_attn_varlen_func(q, k, v, cq, ck, mq, mk, softmax_scale=scale, causal=causal)
+    whole = _unsplit(q, k, v, cq, ck, mq, mk, scale, causal)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again), "split result differs between two calls"
+    ref, absv = _torch_reference(q, k, v, lq, lk, scale, causal)
+    check_attention(out, ref, what=f"split prefill seed {seed}", absv=absv)
+    check_attention(whole, ref, what=f"unsplit prefill seed {seed}", absv=absv)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_store_random(gpu, seed):
+    """The store inside the causal self-attention kernel at random segment
+    lengths, GQA groups, tokens before cu[0] and after cu[n], padding slots and
+    (in some cases) an understated max_seqlen: the caches equal the oracle's
+    store byte for byte, and the attention equals the attention kernel's."""
+    rs = np.random.RandomState(8000 + seed)
+    hkv = int(rs.choice([1, 2, 4, 8]))
+    hq = hkv * int(rs.choice([1, 2, 4, 8]))
+    nseg = int(rs.randint(1, 7))
+    lens = [int(x) for x in rs.randint(1, 1500, nseg)]
+    if rs.randint(3) == 0:
+        lens[int(rs.randint(nseg))] = int(rs.choice([1, 2, 255, 256, 257]))
+    N = sum(lens)
+    lead, tail = int(rs.choice([0, 0, 5])), int(rs.choice([0, 0, 7]))
+    mseq = max(1, max(lens) - (int(rs.randint(1, 200)) if rs.randint(4) == 0 else 0))
+    dtype = _DT[int(rs.randint(2))]
+    scale = float(rs.uniform(0.05, 0.2))
+    rows = N + lead + tail + int(rs.randint(0, 500))
+    T = N + lead + tail
+    print(f"case: prefill store seed={seed} hq={hq} hkv={hkv} lens={lens} lead={lead} tail={tail} "
+          f"max_seqlen={mseq} rows={rows} {dtype}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(300 + seed)
+    q = torch.randn((T, hq, 128), generator=g, device=gpu).to(dtype)
+    k = torch.randn((T, hkv, 128), generator=g, device=gpu).to(dtype)
+    v = torch.randn((T, hkv, 128), generator=g, device=gpu).to(dtype)
+    cu = torch.tensor(lead + np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=gpu)
+    sm = rs.permutation(rows)[:T].astype(np.int64)
+    sm[rs.rand(T) < 0.05] = -1  # padding tokens
+    kc = torch.randn((rows, hkv, 128), generator=g, device=gpu).to(dtype)
+    vc = torch.randn((rows, hkv, 128), generator=g, device=gpu).to(dtype)
+    ke, ve = np_of(kc).copy(), np_of(vc).copy()
+    out = fai.varlen_prefill_with_kvcache(q, k, v, cu, mseq, kc, vc, torch.from_numpy(sm).to(gpu),
+                                          softmax_scale=scale, causal=True)
+    torch.cuda.synchronize()
+    oracle.kv_store(ke, np_of(k), sm)
+    oracle.kv_store(ve, np_of(v), sm)
+    assert _same_bytes(kc, ke), "k cache"
+    assert _same_bytes(vc, ve), "v cache"
+    if mseq == max(lens):  # an understated max_seqlen leaves uncovered rows unwritten
+        seg = slice(lead, lead + N)
+        whole = _unsplit(q, k, v, cu, cu, mseq, mseq, scale, True)
+        torch.cuda.synchronize()
+        assert torch.equal(out[seg].view(torch.int16), whole[seg].view(torch.int16)), \
+            "store variant attention != attention kernel"
+        ref, absv = _torch_reference(q[seg], k[seg], v[seg], lens, lens, scale, True)
+        check_attention(out[seg], ref, what=f"prefill store seed {seed}", absv=absv)
