@@ -550,11 +550,13 @@ def bench_e2e(torch, args):
 # CPU baselines: the reference's semantics in fp32 torch on the host cores
 # (oracle/torch_path.py, oracle/qwen3_ref.py), 3 warm-ups then the median of 5
 # ----------------------------------------------------------------------------
-def _median_time(fn, warmup=3, reps=5):
+def _median_time(fn, warmup=3, reps=5, budget_s=0.0, max_reps=1000):
+    """Median of at least ``reps`` timed runs after ``warmup`` untimed ones,
+    repeated until ``budget_s`` seconds have been timed (at most ``max_reps``)."""
     for _ in range(warmup):
         fn()
     ts = []
-    for _ in range(reps):
+    while len(ts) < reps or (sum(ts) < budget_s and len(ts) < max_reps):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
@@ -586,7 +588,8 @@ def _paged_tables(ctx, bs, rs):
     return bt, pool
 
 
-def cpu_decode_baseline(torch, ctx, hq, hkv, label, threads, dtype=None, d=128, bs=256, seed=3):
+def cpu_decode_baseline(torch, ctx, hq, hkv, label, threads, dtype=None, d=128, bs=256, seed=3,
+                        budget_s=5.0):
     """Paged decode store+attend (model/model.py:233-241) on the host:
     oracle.torch_path.decode_store_attend in fp32 on bf16-valued caches (or
     ``dtype``), the same contexts, 16/8 or 32/8 heads, block 256."""
@@ -604,7 +607,7 @@ def cpu_decode_baseline(torch, ctx, hq, hkv, label, threads, dtype=None, d=128, 
     torch.set_num_threads(threads)
     try:
         med, ts = _median_time(lambda: tp.decode_store_attend(q, kn, vn, kc, vc, bt, ctx - 1,
-                                                              d ** -0.5))
+                                                              d ** -0.5), budget_s=budget_s)
     finally:
         torch.set_num_threads(prev)
     esz = torch.tensor([], dtype=dtype).element_size()
@@ -613,10 +616,10 @@ def cpu_decode_baseline(torch, ctx, hq, hkv, label, threads, dtype=None, d=128, 
                 seconds_per_step=round(med, 4), bytes_per_step=nbytes,
                 sample=f"{label}: store+attend of one decode step (oracle.torch_path, fp32 torch "
                        f"on {str(dtype).split('.')[-1]}-valued caches, {threads} host threads), "
-                       f"median of 5 after 3 warm-ups ({sum(ts):.1f} s timed)")
+                       f"median of {len(ts)} after 3 warm-ups ({sum(ts):.1f} s timed)")
 
 
-def cpu_prefill_baseline(torch, nseq, L, hq, hkv, threads, d=128, bs=256, seed=4):
+def cpu_prefill_baseline(torch, nseq, L, hq, hkv, threads, d=128, bs=256, seed=4, budget_s=5.0):
     """Varlen causal prefill store+attend (llm.py:171-184) on the host:
     index_copy_ into a shuffled paged cache, then torch SDPA per segment in
     fp32 on bf16-valued q/k/v."""
@@ -638,7 +641,7 @@ def cpu_prefill_baseline(torch, nseq, L, hq, hkv, threads, d=128, bs=256, seed=4
     torch.set_num_threads(threads)
     try:
         med, ts = _median_time(lambda: tp.prefill_store_attend(q, k, v, cu, kc, vc, sm,
-                                                               d ** -0.5))
+                                                               d ** -0.5), budget_s=budget_s)
     finally:
         torch.set_num_threads(prev)
     flops = 4 * hq * d * nseq * (L * (L + 1) // 2)
@@ -646,7 +649,7 @@ def cpu_prefill_baseline(torch, nseq, L, hq, hkv, threads, d=128, bs=256, seed=4
                 seconds_per_call=round(med, 4),
                 sample=f"varlen causal prefill {nseq} x {L}, {hq}/{hkv} heads: index_copy_ store "
                        f"+ torch SDPA per segment (oracle.torch_path, fp32 on bf16-valued inputs, "
-                       f"{threads} host threads), median of 5 after 3 warm-ups "
+                       f"{threads} host threads), median of {len(ts)} after 3 warm-ups "
                        f"({sum(ts):.1f} s timed)")
 
 
@@ -943,7 +946,8 @@ def main():
         n = cpu_threads()
         line["cpu_baseline"] = cpu_decode_baseline(
             torch, dec["x"]["ctx"], 16, 8, f"256 seqs x context U[1024,2047] (the same "
-            f"{int(dec['x']['ctx'].sum())} context tokens), 16/8 heads, block 256", n)
+            f"{int(dec['x']['ctx'].sum())} context tokens), 16/8 heads, block 256", n,
+            budget_s=10.0)
         line["cpu_baseline"]["host_cpus_visible"] = len(os.sched_getaffinity(0))
         line["cpu_baseline"]["oracle_1core"] = oracle_1core(dec["x"], reps=5)
         if "decode_fp32_small" in res:

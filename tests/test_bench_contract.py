@@ -3,6 +3,7 @@ count of a decode step, and the CPU-baseline leg on a tiny sample."""
 import os
 import subprocess
 import sys
+import time
 
 import numpy as np
 
@@ -51,12 +52,21 @@ def test_cpu_path_baselines_run_on_the_host_threads():
     small engine run report a rate, the threads used and what was timed."""
     import torch
     ctx = np.array([5, 300, 1, 77], np.int32)
-    r = bench.cpu_decode_baseline(torch, ctx, 4, 2, "tiny", threads=2)
+    r = bench.cpu_decode_baseline(torch, ctx, 4, 2, "tiny", threads=2, budget_s=0.2)
     assert r["unit"] == "GB/s" and r["cores"] == 2 and r["kind"] == "port" and r["value"] > 0
     assert r["bytes_per_step"] == int(ctx.sum()) * 2 * 128 * 2 * 2 + 2 * 4 * 4 * 128 * 2 + \
         4 * 4 * 2 * 128 * 2
-    p = bench.cpu_prefill_baseline(torch, 2, 300, 4, 2, threads=2)
+    p = bench.cpu_prefill_baseline(torch, 2, 300, 4, 2, threads=2, budget_s=0.2)
     assert p["unit"] == "TFLOP/s" and p["value"] > 0 and "2 x 300" in p["sample"]
+
+
+def test_cpu_timing_repeats_until_its_budget():
+    calls = []
+    med, ts = bench._median_time(lambda: calls.append(time.sleep(0.01)), warmup=1, reps=2,
+                                 budget_s=0.1)
+    assert len(calls) == 1 + len(ts) and len(ts) >= 5 and sum(ts) >= 0.1
+    med, ts = bench._median_time(lambda: None, warmup=0, reps=3, budget_s=10.0, max_reps=7)
+    assert len(ts) == 7
 
 
 def test_traffic_summaries_are_read_from_profiles():
