@@ -80,6 +80,7 @@ TRAFFIC_PROFILE = "profiles/decode_256seq_ctx1k-2k_bf16_traffic.md"
 TRAFFIC_PREFILL = "profiles/prefill_8x1024_bf16_traffic.md"
 TRAFFIC_DECODE_LONG = "profiles/decode_long_64seq_ctx16k-32k_bf16_traffic.md"
 TRAFFIC_KV_EXPORT = "profiles/kv_export_2048tok_28layers_bf16_traffic.md"
+DEVICE_PROFILE = "profiles/device_mi355x.md"
 
 
 def measured_traffic(profile=TRAFFIC_PROFILE, key="traffic_bytes_per_launch"):
@@ -809,6 +810,14 @@ def cpu_e2e_baseline(torch, ctx, threads, reps=3, seed=2, hidden=1024, inter=307
                 seconds_per_step=round(step, 3))
 
 
+def device_record(torch, dev):
+    """The GPU the line was measured on (the clock and the peak derivation are
+    in profiles/device_mi355x.md)."""
+    p = torch.cuda.get_device_properties(dev)
+    return {"arch": p.gcnArchName.split(":")[0], "compute_units": p.multi_processor_count,
+            "memory_gib": round(p.total_memory / 2 ** 30, 1), "properties": DEVICE_PROFILE}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -887,6 +896,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v and caches, random shuffled block tables)",
+        "device": device_record(torch, dev),
         "config": {
             "workload": "paged decode store+attend, 256 seqs, 16 q / 8 kv heads, head_dim 128, "
                         "context U[1024,2047], block 256, shared shuffled pool",
