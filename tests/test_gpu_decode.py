@@ -305,3 +305,48 @@ def test_decode_long_context_all_sequences_vs_torch_fp32(gpu):
         worst = max(worst, float(err.max()))
     assert worst <= 2e-2
     print(f"max-abs error over all 64 sequences {worst:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,part", [
+    (torch.bfloat16, 16, 8, 0), (torch.bfloat16, 32, 8, 512), (torch.float16, 16, 8, 256),
+    (torch.float32, 16, 8, 0)])
+def test_decode_constant_values_return_that_value(gpu, dtype, hq, hkv, part):
+    """Every cached V row of KV head h equal to u_h (and the appended one too):
+    each query head returns u_h, whatever the scores and the partitioning
+    (split-K partials merged by their log-sum-exp).  bf16/fp16: within one
+    unit in the last place (the probabilities are rounded before the PV
+    product and the row sum is taken over the rounded values); fp32: within
+    1e-5 relative, the bound of the other fp32 checks (the PV sum and the row
+    sum add the same terms in different orders)."""
+    print(f"case: decode constant V {dtype} hq={hq} hkv={hkv} part={part}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(12)
+    rs = np.random.RandomState(12)
+    B, bs = 24, 64
+    ctx = rs.randint(1, 3000, B).astype(np.int32)
+    ctx[:3] = [1, bs, bs + 1]
+    need = -(-ctx // bs)
+    pool = int(need.sum()) + 3
+    perm = rs.permutation(pool).astype(np.int32)
+    bt = np.zeros((B, int(need.max())), np.int32)
+    k0 = 0
+    for b in range(B):
+        bt[b, :need[b]] = perm[k0:k0 + need[b]]
+        k0 += need[b]
+    u = torch.randn((hkv, 128), generator=g, device=gpu).to(dtype)
+    kc = torch.randn((pool, bs, hkv, 128), generator=g, device=gpu).to(dtype)
+    vc = u.expand(pool, bs, hkv, 128).contiguous()
+    q = (3.0 * torch.randn((B, 1, hq, 128), generator=g, device=gpu)).to(dtype)
+    kn = torch.randn((B, 1, hkv, 128), generator=g, device=gpu).to(dtype)
+    vn = u.expand(B, 1, hkv, 128).contiguous()
+    seqlens = torch.from_numpy(ctx - 1).to(gpu)
+    mcl = int(ctx.max())
+    out = fai.flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens,
+                                      block_table=torch.from_numpy(bt).to(gpu),
+                                      num_splits=(mcl // part if part else 0))
+    torch.cuda.synchronize()
+    want = u.repeat_interleave(hq // hkv, dim=0).float().expand(B, hq, 128)
+    err = (out.view(B, hq, 128).float() - want).abs()
+    ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 1e-5}[dtype]
+    bad = err > ulp * want.abs()
+    assert not bad.any(), f"{int(bad.sum())} values beyond one ulp (max err {float(err.max()):.3e})"
+    print(f"  exact: {bool((err == 0).all())}, max err {float(err.max()):.3e}", flush=True)

@@ -325,3 +325,37 @@ def test_split_workspace_reused_by_a_call_with_more_items(gpu):
         torch.cuda.synchronize()
         assert torch.isfinite(out.float()).all()
         assert float((out.float() - base.float()).abs().max()) <= 2 ** -6
+
+
+@pytest.mark.parametrize("hq,hkv,dtype,causal,lens", [
+    (16, 8, torch.bfloat16, True, [1024] * 8),             # the 8 x 1024 layer
+    (32, 8, torch.bfloat16, True, [3000, 17, 700]),         # GQA-4, ragged
+    (16, 8, torch.float16, False, [300, 1500]),            # fp16, non-causal
+    (16, 8, torch.bfloat16, True, [2048]),                  # one request: split key ranges
+])
+def test_constant_values_return_that_value(gpu, hq, hkv, dtype, causal, lens):
+    """Every V row of KV head h equal to one vector u_h: every query row returns
+    u_h (its softmax weights sum to one), whatever the scores.  The kernel
+    normalises by the row sum of the very probabilities it rounds for the PV
+    product, so the result is u_h to the last bit; a dropped, doubled or
+    misplaced key, tile or split piece, or a row sum taken over other
+    probabilities, moves it."""
+    print(f"case: constant V hq={hq} hkv={hkv} {dtype} causal={causal} lens={lens}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(11)
+    N = sum(lens)
+    q = (3.0 * torch.randn((N, hq, 128), generator=g, device=gpu)).to(dtype)
+    k = torch.randn((N, hkv, 128), generator=g, device=gpu).to(dtype)
+    u = torch.randn((hkv, 128), generator=g, device=gpu).to(dtype)
+    v = u.expand(N, hkv, 128).contiguous()
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=gpu)
+    want = u.repeat_interleave(hq // hkv, dim=0).expand(N, hq, 128)
+    outs = {"varlen": fai.flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), causal=causal)}
+    if causal:
+        kc = torch.zeros((N, hkv, 128), dtype=dtype, device=gpu)
+        vc = torch.zeros_like(kc)
+        slots = torch.randperm(N, generator=g, device=gpu)
+        outs["with store"] = fai.varlen_prefill_with_kvcache(q, k, v, cu, max(lens), kc, vc, slots)
+    torch.cuda.synchronize()
+    for name, out in outs.items():
+        assert torch.equal(out, want), \
+            f"{name}: max |out - u| = {float((out.float() - want.float()).abs().max()):.3e}"

@@ -110,3 +110,43 @@ def test_prefill_and_decode_slot_mappings_agree(lens, block_size, seed):
     # appending the next token never collides with a prefilled row
     nxt = paged.decode_slot_mapping(bt, lens, block_size)
     assert not set(nxt.tolist()) & set(pre.tolist())
+
+
+@SETTINGS
+@given(
+    segs=st.lists(st.tuples(st.integers(1, 9), st.integers(0, 9)), min_size=1, max_size=3),
+    hkv=st.sampled_from([1, 2]),
+    g=st.sampled_from([1, 2, 4]),
+    causal=st.booleans(),
+    seed=st.integers(0, 2**16),
+)
+def test_oracle_constant_values_return_that_value(segs, hkv, g, causal, seed):
+    """Every V row of KV head h equal to one vector u_h: each query row that
+    sees a key returns u_h (the softmax weights sum to one), in the varlen
+    attention and in the paged decode, whatever the scores."""
+    rs = np.random.RandomState(seed)
+    d = 8
+    lq = [a for a, _ in segs]
+    lk = [max(a, b) if causal else max(b, 1) for a, b in segs]  # every row sees a key
+    cq = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    ck = np.concatenate([[0], np.cumsum(lk)]).astype(np.int32)
+    u = rs.standard_normal((hkv, d))
+    q = 3.0 * rs.standard_normal((cq[-1], hkv * g, d))
+    k = rs.standard_normal((ck[-1], hkv, d))
+    v = np.broadcast_to(u, (ck[-1], hkv, d)).copy()
+    got = oracle.varlen_attention(q, k, v, cq, ck, scale=0.9, causal=causal)
+    np.testing.assert_allclose(got, np.repeat(u, g, axis=0)[None].repeat(cq[-1], 0),
+                               rtol=1e-12, atol=1e-12)
+    # paged decode over the same keys of segment 0, scattered over shuffled blocks
+    bs = 4
+    n = lk[0]
+    nb = -(-n // bs)
+    perm = rs.permutation(nb + 2)
+    kc = rs.standard_normal((nb + 2, bs, hkv, d))
+    vc = rs.standard_normal((nb + 2, bs, hkv, d))
+    for t in range(n):
+        kc[perm[t // bs], t % bs] = k[t]
+        vc[perm[t // bs], t % bs] = u
+    qd = rs.standard_normal((1, hkv * g, d))
+    got_d = oracle.paged_decode(qd, kc, vc, perm[None, :nb].astype(np.int32), np.array([n]), bs, 0.9)
+    np.testing.assert_allclose(got_d[0], np.repeat(u, g, axis=0), rtol=1e-12, atol=1e-12)
