@@ -15,7 +15,10 @@
 // wavefronts of a workgroup moves one token row (Hkv * D * elem bytes, 2 KiB
 // for Qwen3 bf16) of one layer's K or V with 16-byte accesses, all loads of a
 // lane before its stores.  Pure data movement: HBM-bound, 2 * row bytes per
-// (layer, K/V, token) moved (read + write).
+// (layer, K/V, token) moved (read + write).  The stores are non-temporal:
+// nothing on the GPU reads the destination soon, and streaming stores lift
+// this mixed read/write traffic from the 5.4 TB/s of a plain device copy to
+// about 7 TB/s (measured on MI355X).
 //
 // Block-table entries outside [0, num_blocks) export zeros and are never
 // written by the import (as the KV store skips invalid slots).
@@ -72,9 +75,9 @@ __global__ __launch_bounds__(256) void kv_xfer_kernel(XferArgs a) {
       const int c = c0 + i * 64 + lane;
       if (c < a.row_chunks) {
         if (EXPORT)
-          *reinterpret_cast<u32x4*>(brow + c * 16) = v[i];
+          __builtin_nontemporal_store(v[i], reinterpret_cast<u32x4*>(brow + c * 16));
         else if (ok)
-          *reinterpret_cast<u32x4*>(crow + c * 16) = v[i];
+          __builtin_nontemporal_store(v[i], reinterpret_cast<u32x4*>(crow + c * 16));
       }
     }
   }
