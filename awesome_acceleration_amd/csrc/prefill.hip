@@ -706,7 +706,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
     {
       // All eight rows are read back before any store, and the stores go
       // through a buffer resource that ends after the segment's last valid
-      // row, so rows past it are dropped without a branch per row.
+      // row, so rows past it are dropped without a branch per row.  They are
+      // non-temporal (cache policy nt): 1-2% faster at 8 x 1024 than plain
+      // stores, measured on MI355X.
+      constexpr int kNt = 2;
       const int row0 = cur.qb * BQ + wq * 32;  // the wave's first query
       const int nrow = min(32, cur.Lq - row0);
       u16* og = a.out + (int64_t)(cur.q_beg + row0) * a.o_stride + (cur.h * G + wh) * D;
@@ -720,7 +723,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
       const int voff = (lane >> 4) * ostep + (lane & 15) * 16;
 #pragma unroll
       for (int it = 0; it < 8; ++it)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val[it]), ors, voff, 4 * it * ostep, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val[it]), ors, voff, 4 * it * ostep, kNt);
     }
     }  // emit
     if (STORE) {
