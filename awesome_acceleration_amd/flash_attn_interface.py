@@ -82,47 +82,47 @@ def _token_rows(t: torch.Tensor, name: str) -> int:
 
 # ---------------------------------------------------------------- workspace
 _ws_lock = threading.Lock()
-_ws: dict[int, torch.Tensor] = {}
+_ws: dict[tuple[int, int], torch.Tensor] = {}
+_pf_ws: dict[tuple[int, int], torch.Tensor] = {}
 _ws_retired: list[torch.Tensor] = []
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    """Per-device scratch for split-K partials, grown on demand.
-
-    A buffer that is outgrown is kept alive rather than freed: a captured
-    HIP graph may hold its address.  Calls that overlap on different streams
-    of one device would share it; the reference issues every attention call
-    from one thread on one stream.
-    """
+def _stream_key(device: torch.device) -> tuple[int, int]:
     idx = device.index if device.index is not None else torch.cuda.current_device()
+    return idx, torch.cuda.current_stream(idx).cuda_stream
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Scratch for split-K decode partials, one per (device, stream), grown on
+    demand: calls on different streams never share partials.  A buffer that
+    is outgrown is kept alive rather than freed: a captured HIP graph may hold
+    its address."""
+    key = _stream_key(device)
     with _ws_lock:
-        buf = _ws.get(idx)
+        buf = _ws.get(key)
         if buf is None or buf.numel() < nbytes:
             if buf is not None:
                 _ws_retired.append(buf)
             buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-            _ws[idx] = buf
+            _ws[key] = buf
         return buf
 
 
-_pf_ws: dict[int, torch.Tensor] = {}
-
-
 def _prefill_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    """Per-device workspace of the split-key prefill: zero-filled when it is
-    allocated (its leading per-item counters must start at zero; every call
-    leaves them at zero), grown on demand, and never shared with the decode
-    workspace.  Outgrown buffers stay alive (a captured graph may hold them).
-    Like the decode workspace it is one buffer per device: prefills that
-    overlap on different streams of one device would share its counters."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
+    """Workspace of the split-key prefill, one per (device, stream): zero-filled
+    (by a fill kernel) when it is allocated, since its leading per-item
+    counters must start at zero and every call leaves them at zero; grown on
+    demand, never shared with the decode workspace, and outgrown buffers stay
+    alive (a captured graph may hold them).  Per stream, so prefills that
+    overlap on two streams never count into each other's counters."""
+    key = _stream_key(device)
     with _ws_lock:
-        buf = _pf_ws.get(idx)
+        buf = _pf_ws.get(key)
         if buf is None or buf.numel() < nbytes:
             if buf is not None:
                 _ws_retired.append(buf)
             buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-            _pf_ws[idx] = buf
+            _pf_ws[key] = buf
         return buf
 
 

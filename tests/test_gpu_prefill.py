@@ -359,3 +359,36 @@ def test_constant_values_return_that_value(gpu, hq, hkv, dtype, causal, lens):
     for name, out in outs.items():
         assert torch.equal(out, want), \
             f"{name}: max |out - u| = {float((out.float() - want.float()).abs().max()):.3e}"
+
+
+def test_split_prefills_on_two_streams_keep_their_own_workspaces(gpu):
+    """Two split-key prefills launched on two streams with nothing ordering
+    them: each stream has its own workspace (per-item counters and partial
+    results), so each result equals the same call made alone, bit for bit."""
+    print("case: split prefills on two streams", flush=True)
+    from awesome_acceleration_amd import _lib
+    a = _ragged([2048], [2048], 16, 8, torch.bfloat16, gpu, seed=51)
+    b = _ragged([1536], [1536], 16, 8, torch.bfloat16, gpu, seed=52)
+    assert _lib.lib().aac_prefill_workspace_bytes(1, 2048, 2048, 16, 8, 128, 1) > 0
+    assert _lib.lib().aac_prefill_workspace_bytes(1, 1536, 1536, 16, 8, 128, 1) > 0
+
+    def call(x):
+        q, k, v, cq, ck = x
+        L = int((cq[1:] - cq[:-1]).max())
+        return fai.flash_attn_varlen_func(q, k, v, cq, ck, L, L, causal=True)
+
+    alone = (call(a), call(b))
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(device=gpu), torch.cuda.Stream(device=gpu)
+    for rnd in range(4):
+        s1.wait_stream(torch.cuda.current_stream(gpu))
+        s2.wait_stream(torch.cuda.current_stream(gpu))
+        with torch.cuda.stream(s1):
+            o1 = call(a)
+        with torch.cuda.stream(s2):
+            o2 = call(b)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, alone[0]), f"stream 1, round {rnd}"
+        assert torch.equal(o2, alone[1]), f"stream 2, round {rnd}"
+    keys = {k for k in fai._pf_ws if k[0] == gpu.index or gpu.index is None}
+    assert {s1.cuda_stream, s2.cuda_stream} <= {k[1] for k in keys}
