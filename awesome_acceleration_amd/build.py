@@ -36,6 +36,17 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-file device code-generation options.  The wide prefill kernel runs one
+# wave per SIMD with 512 registers: its score MFMAs must write ordinary VGPRs
+# (the softmax reads them) while MFMA-only operands (Q, the K/V fragments)
+# live in AGPRs.  By default the backend gives every MFMA of such a kernel an
+# AGPR destination and copies the scores back, ~100 copies per sub-tile;
+# the VGPR form lets its register allocator place each operand instead.
+FILE_FLAGS = {
+    "prefill_wide.hip": ["-Xarch_device", "-mllvm=-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -49,7 +60,8 @@ def sources() -> list[Path]:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+           str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,0 +1,433 @@
+// Varlen causal GQA prefill, "wide" form (gfx950, bf16/fp16 MFMA): the same
+// call as prefill.hip (flash_attn_varlen_func(q, k, v, cu, cu, max, max,
+// causal), llm.py:178-184) for GQA groups of 2, 4 and 8.
+//
+// Why a second kernel.  With one 32-query column per wave (prefill.hip) every
+// MFMA reads its K or V^T fragment from LDS for that column alone, and the
+// softmax of a wave runs beside MFMAs only when the other wave of its SIMD
+// happens to be in its MFMA phase.  Here a workgroup is four waves, one per
+// SIMD, and each wave owns TWO columns: the same 32 queries for two query
+// heads of one KV head.  Two consequences:
+//   * every K / V fragment read from LDS feeds two MFMAs (one per column),
+//     halving the LDS reads per MFMA;
+//   * the two columns run half a sub-tile apart inside the wave's own
+//     instruction stream (an in-wave ping-pong): while the MFMAs of column c
+//     compute the next scores S_c(j+1) and the product O_c += V(j) P_c(j), the
+//     VALU and transcendental units run the softmax of the other column on
+//     scores already computed.  Neither half waits for the other, so the
+//     MFMA pipe is fed from one wave without another wave's help.
+// With 512 registers per lane at one wave per SIMD the O accumulators of both
+// columns (128 registers) sit beside Q (64), the shared fragments (64) and the
+// scores and probabilities of both columns.
+//
+// Sub-tile j = 32 keys; per j the wave runs two slots:
+//   slot A(j): MFMA  S_0(j+1) = K(j+1) Q_0^T,  O_0 += V(j)^T P_0(j)
+//              VALU  softmax of S_1(j) -> P_1(j)
+//   slot B(j): MFMA  S_1(j+1) = K(j+1) Q_1^T,  O_1 += V(j)^T P_1(j)
+//              VALU  softmax of S_0(j+1) -> P_0(j+1)
+// The K(j+1) and V(j) fragments are read once, used in both slots, and each
+// register is refilled for sub-tiles j+2 / j+1 right after its last use in
+// slot B.  Row sums of the rounded probabilities come from a 16x16x32 MFMA
+// with a constant selector operand (two per column and sub-tile) instead of
+// VALU or v_dot2 work.
+//
+// Staging: K and V tiles (64 keys) go from global memory straight into LDS
+// (buffer_load_dwordx4 ... lds: 1 KiB per wave instruction, no registers,
+// no VALU), four stages deep.  K rows are stored with their 16-byte chunks
+// XOR-swizzled by the row (chunk c of row r at c ^ (r & 15)), so the score
+// MFMA's fragment reads (32 rows, one chunk) spread over all banks.  V rows
+// are stored row-major (chunk c of row r at c ^ 4 (r & 3)) and read with the
+// transposing LDS load ds_read_b64_tr_b16, which hands every lane four keys
+// of one dimension -- exactly the V^T operand of the P*V MFMA -- so V needs
+// no transpose on the way in.
+//
+// Everything else follows prefill.hip: scores transposed (S^T = K Q^T,
+// v_mfma_f32_32x32x16) so a lane holds one query column, the probabilities
+// already in the B-operand layout of O^T += V^T P^T, online softmax in the
+// log2 domain with lazy rescaling, bottom-right causal alignment, buffer
+// resources that zero-fill past the visible keys, and the persistent
+// heavy-first zigzag grid.
+//
+// FLOPs per launch (the MFMA roofline): 4 * Hq * D * (visible query/key pairs).
+
+#include <algorithm>
+
+#include "prefill_common.h"
+#include "prefill_wide.h"
+#include "prefill_wide_asm.inc"
+
+// Registers the item body keeps its own values in (see gen_prefill_wide_asm.py).
+#define AAC_PW_CLOBBERS \
+  "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159", "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "a0", "a1", "a2", "a3", "a4", "a5", "a6", "a7", "a8", "a9", "a10", "a11", "a12", "a13", "a14", "a15", "a16", "a17", "a18", "a19", "a20", "a21", "a22", "a23", "a24", "a25", "a26", "a27", "a28", "a29", "a30", "a31", "a32", "a33", "a34", "a35", "a36", "a37", "a38", "a39", "a40", "a41", "a42", "a43", "a44", "a45", "a46", "a47", "a48", "a49", "a50", "a51", "a52", "a53", "a54", "a55", "a56", "a57", "a58", "a59", "a60", "a61", "a62", "a63", "a64", "a65", "a66", "a67", "a68", "a69", "a70", "a71", "a72", "a73", "a74", "a75", "a76", "a77", "a78", "a79", "a80", "a81", "a82", "a83", "a84", "a85", "a86", "a87", "a88", "a89", "a90", "a91", "a92", "a93", "a94", "a95", "a96", "a97", "a98", "a99", "a100", "a101", "a102", "a103", "a104", "a105", "a106", "a107", "a108", "a109", "a110", "a111", "a112", "a113", "a114", "a115", "a116", "a117", "a118", "a119", "a120", "a121", "a122", "a123", "a124", "a125", "a126", "a127", "a128", "a129", "a130", "a131", "a132", "a133", "a134", "a135", "a136", "a137", "a138", "a139", "a140", "a141", "a142", "a143", "a144", "a145", "a146", "a147", "a148", "a149", "a150", "a151", "a152", "a153", "a154", "a155", "a156", "a157", "a158", "a159", "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172", "a173", "a174", "a175", "a176", "a177", "a178", "a179", "a180", "a181", "a182", "a183", "a184", "a185", "a186", "a187", "a188", "a189", "a190", "a191", "a192", "a193", "a194", "a195", "a196", "a197", "a198", "a199", "a200", "a201", "a202", "a203", "a204", "a205", "a206", "a207", "a208", "a209", "a210", "a211", "a212", "a213", "a214", "a215", "a216", "a217", "a218", "a219", "a220", "a221", "a222", "a223", "vcc", "m0", "scc", "memory"
+
+namespace aac {
+namespace pw {
+
+using pf::Args;
+using pf::BKV;
+using pf::D;
+using pf::OPITCH;
+using pf::kRescale;
+
+constexpr int kWaves = 4;  // one per SIMD
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRing = 4;                   // LDS stages
+constexpr int kTileBytes = BKV * D * 2;    // 16 KiB: one K or V tile
+constexpr int kStageBytes = 2 * kTileBytes;
+constexpr int kLdsBytes = kRing * kStageBytes;  // 128 KiB
+constexpr int kLoadsPerTile = 8;           // direct loads per thread per tile (4 K + 4 V)
+
+template <bool F16> struct Sel;
+// 16x16x32 MFMA for the row sums: A is a constant selector, B the probability
+// fragment of one 16-key step (the B operand of the P*V product).
+template <> struct Sel<false> {
+  __device__ static inline f32x4 run(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static constexpr u32 kOnes = 0x3f803f80u;
+};
+template <> struct Sel<true> {
+  __device__ static inline f32x4 run(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static constexpr u32 kOnes = 0x3c003c00u;
+};
+
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// 16 bytes from global memory (buffer resource, 32-bit offsets) straight into
+// LDS at m0 + 16 * lane.  The load is issued from inline assembly: the
+// compiler then does not count it, so the waits for it are explicit (see the
+// tile loop); m0 is set right before it and used by nothing else here.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, int voff, int soff, u32 lds_dst) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(soff), "s"(lds_dst)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+template <int G, bool CAUSAL, bool F16>
+__global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
+  static_assert(G == 2 || G == 4 || G == 8, "two heads of one KV head per wave");
+  constexpr int WP = G / 2;          // head pairs per workgroup
+  constexpr int WQ = kWaves / WP;    // 32-query slots per workgroup
+  constexpr int BQ = 32 * WQ;
+  typedef pf::Mfma<F16> M;
+  typedef Sel<F16> SM;
+
+  // LDS: kRing stages of [K tile | V tile]; after each item the ring stages
+  // the output tile (eight 32-row blocks of padded 256-byte rows).
+  static_assert(kWaves * 2 * 32 * OPITCH * 2 <= kLdsBytes, "output staging fits in the ring");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[kLdsBytes];
+  const u32 lds0 = (u32)(uintptr_t)(lds_u8*)lds;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wq = wave % WQ, wp = wave / WQ;  // query slot, head pair
+  const int hl = lane >> 5;
+  const int col = lane & 31;
+
+  // ---- direct loads: instruction i of wave w fills LDS rows 16 i + 4 w +
+  // lane/16 (1 KiB), lane%16 = the LDS chunk slot of its row, read from the
+  // global chunk that the row's swizzle puts there.
+  const int k_row_bytes = (int)(a.k_stride * 2), v_row_bytes = (int)(a.v_stride * 2);
+  const int r4 = 4 * wave + (lane >> 4);
+  const int ld_voff_k = r4 * k_row_bytes + 16 * ((lane & 15) ^ (r4 & 15));
+  const int ld_voff_v = r4 * v_row_bytes + 16 * ((lane & 15) ^ (4 * (lane >> 4)));
+
+  // ---- per-lane LDS read offsets (bytes within a stage's tile).
+  // K (A operand of S^T = K Q^T): row col (+32 for the second sub-tile of a
+  // tile), dims 16 t + 8 hl .. +7, i.e. logical chunk 2 t + hl.
+  int koff[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) koff[t] = col * 256 + 16 * ((2 * t + hl) ^ (col & 15));
+  // V (A operand of O^T = V^T P^T through ds_read_b64_tr_b16): in each
+  // 16-lane group g, lane i supplies row 4 (g>>1) + (i>>2) (keys; +8 for the
+  // second read of a fragment, +16 per 16-key step), dims 32 db + 16 (g&1) +
+  // 4 (i&3) .. +3; the read then gives lane j of the group the four keys
+  // 4 (g>>1) + 0..3 of dim 32 db + 16 (g&1) + j -- the B-operand key order of
+  // the probabilities (keys 4 hl + 0..3, then 8 + 4 hl + 0..3).
+  int voff[4];
+  {
+    const int g = lane >> 4, i = lane & 15;
+    const int l0 = (4 * (g >> 1) + (i >> 2)) * 256 + 32 * (g & 1) + 8 * (i & 3);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) voff[db] = l0 + 64 * (db ^ (i >> 2));
+  }
+  // selector of the row-sum MFMA: A[0][k] = 1 for k in [0,8) u [16,24) (the
+  // probabilities of queries 0-15), A[1][k] = 1 for k in [8,16) u [24,32)
+  // (queries 16-31); lane l holds A[l%16][8 (l/16) ..+7]
+  u32x4 sel;
+  {
+    const bool one = lane == 0 || lane == 32 || lane == 17 || lane == 49;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sel[i] = one ? SM::kOnes : 0u;
+  }
+
+  // ---- work items (q-block rank z, segment s, KV head h), rank-major so the
+  // heaviest causal q-blocks come first.  Persistent grid: workgroup w of P
+  // takes item k P + w in even rounds and, in odd rounds, the mirror image
+  // taken in groups of eight (item (k+1) P - 8 - 8 (w/8) + w%8 when P is a
+  // multiple of 8): heavy items pair with light ones, and item i mod 8 stays
+  // equal to w mod 8, so with eight KV heads each head's K/V rows are read
+  // by one XCD's workgroups (workgroups are dealt to the 8 XCDs round-robin).
+  struct Item {
+    int h, s, qb, q_beg, Lq, k_beg, Lk;
+  };
+  const int n_hs = a.hkv * a.n_seqs;
+  const int n_items = n_hs * a.n_qblocks;
+  const int P = gridDim.x, w = blockIdx.x;
+  auto item_index = [&](int k) {
+    if (!(k & 1)) return k * P + w;
+    return (P & 7) == 0 ? (k + 1) * P - 8 - (w & ~7) + (w & 7) : (k + 1) * P - 1 - w;
+  };
+  auto seg_of = [&](int i) { return (i % n_hs) / a.hkv; };
+  auto kv_end_of = [&](const Item& it) {
+    const int wg_qmax = min(it.qb * BQ + BQ, it.Lq) - 1;
+    return CAUSAL ? max(0, min(it.Lk, wg_qmax + 1 + it.Lk - it.Lq)) : it.Lk;
+  };
+  auto decode = [&](int i, int q0, int q1, int k0, int k1, Item& it) -> bool {
+    const int z = i / n_hs;
+    const int hs = i - z * n_hs;
+    it.s = hs / a.hkv;
+    it.h = hs - it.s * a.hkv;
+    it.q_beg = q0;
+    it.Lq = q1 - q0;
+    it.k_beg = k0;
+    it.Lk = min(k1 - k0, a.max_k);
+    const int nqb = (it.Lq + BQ - 1) / BQ;
+    it.qb = CAUSAL ? nqb - 1 - z : z;
+    return z < nqb;
+  };
+  auto next_item = [&](int& k, Item& it) -> bool {
+    for (; k * P < n_items; ++k) {
+      const int i = item_index(k);
+      if (i >= n_items) continue;
+      const int sg = seg_of(i);
+      if (decode(i, a.cu_q[sg], a.cu_q[sg + 1], a.cu_k[sg], a.cu_k[sg + 1], it)) return true;
+    }
+    return false;
+  };
+  auto rsrc_of = [&](const u16* base, int row_bytes, int kv_end) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(base), 0,
+                                             kv_end > 0 ? (kv_end - 1) * row_bytes + D * 2 : 0,
+                                             0x00020000);
+  };
+
+  // Q fragments of both columns (B operand of S^T = K Q^T; lane = query).
+  // The 16 loads are issued from inline assembly: the compiler then does not
+  // track them and does not wait for them (and so for every tile load issued
+  // after them) ahead of the item body.  They are older than the item's tile
+  // loads, so the wait for tile 0 before the item's first barrier covers them.
+  u32x4 qf[2][8];
+  auto load_q = [&](const Item& it) {
+    const int qi = it.qb * BQ + wq * 32 + col;
+    const int qrow = it.q_beg + min(qi, max(it.Lq - 1, 0));
+    const u16* qp = a.q + (int64_t)qrow * a.q_stride + (it.h * G + 2 * wp) * D + hl * 8;
+    asm volatile(
+        "global_load_dwordx4 %0, %16, off\n\tglobal_load_dwordx4 %1, %16, off offset:32\n\t"
+        "global_load_dwordx4 %2, %16, off offset:64\n\tglobal_load_dwordx4 %3, %16, off offset:96\n\t"
+        "global_load_dwordx4 %4, %16, off offset:128\n\tglobal_load_dwordx4 %5, %16, off offset:160\n\t"
+        "global_load_dwordx4 %6, %16, off offset:192\n\tglobal_load_dwordx4 %7, %16, off offset:224\n\t"
+        "global_load_dwordx4 %8, %16, off offset:256\n\tglobal_load_dwordx4 %9, %16, off offset:288\n\t"
+        "global_load_dwordx4 %10, %16, off offset:320\n\tglobal_load_dwordx4 %11, %16, off offset:352\n\t"
+        "global_load_dwordx4 %12, %16, off offset:384\n\tglobal_load_dwordx4 %13, %16, off offset:416\n\t"
+        "global_load_dwordx4 %14, %16, off offset:448\n\tglobal_load_dwordx4 %15, %16, off offset:480"
+        : "=&v"(qf[0][0]), "=&v"(qf[0][1]), "=&v"(qf[0][2]), "=&v"(qf[0][3]), "=&v"(qf[0][4]),
+          "=&v"(qf[0][5]), "=&v"(qf[0][6]), "=&v"(qf[0][7]), "=&v"(qf[1][0]), "=&v"(qf[1][1]),
+          "=&v"(qf[1][2]), "=&v"(qf[1][3]), "=&v"(qf[1][4]), "=&v"(qf[1][5]), "=&v"(qf[1][6]),
+          "=&v"(qf[1][7])
+        : "v"(qp)
+        : "memory");
+  };
+
+  int k = 0;
+  Item cur;
+  if (!next_item(k, cur)) return;
+  int kv_end = kv_end_of(cur);
+  __amdgpu_buffer_rsrc_t rsk, rsv;
+  auto set_rsrc = [&](const Item& it) {
+    rsk = rsrc_of(a.k + (int64_t)it.k_beg * a.k_stride + it.h * D, k_row_bytes, kv_end);
+    rsv = rsrc_of(a.v + (int64_t)it.k_beg * a.v_stride + it.h * D, v_row_bytes, kv_end);
+  };
+  set_rsrc(cur);
+
+  // tile T of the current item into stage T % kRing (past the last tile the
+  // resource range check reads zeros)
+  auto issue_tile = [&](int T) {
+    const u32 st = lds0 + (u32)((T % kRing) * kStageBytes) + (u32)(wave * 1024);
+    const int sk = T * BKV * k_row_bytes, sv = T * BKV * v_row_bytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      load_lds16(rsk, ld_voff_k, sk + i * 16 * k_row_bytes, st + i * 4096);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      load_lds16(rsv, ld_voff_v, sv + i * 16 * v_row_bytes, st + kTileBytes + i * 4096);
+  };
+  // the loads of all but the newest `n` tiles of this thread have landed
+  auto wait_tiles = [&](int n) {
+    if (n == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  // barrier without the compiler's full fence (which would also wait for
+  // every load in flight); LDS accesses are not moved across it
+  auto barrier = [&]() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+
+  const float cs = a.scale_log2;
+  const float ncs = -cs;
+  const float kthr = kRescale / cs;
+  // per-lane constants of the item body: 4 hl (key offset of the lane half),
+  // bpermute addresses of lanes (lane & 15) and (lane & 15) + 16, the lane's
+  // bit 4, and the byte address of this lane's first output element in the
+  // LDS staging area (wave's two 32-row blocks, row col, dims 4 hl ..)
+  const int hl4 = 4 * hl;
+  const int bpa = (lane & 15) * 4, bpahi = ((lane & 15) + 16) * 4, hi16 = lane & 16;
+  const int obase = (int)lds0 + ((wave * 2) * 32 * OPITCH + col * OPITCH + 4 * hl) * 2;
+  const u32 ldsw = lds0 + (u32)(wave * 1024);
+  const int ks16 = 16 * k_row_bytes, vs16 = 16 * v_row_bytes;
+  const int ks64 = 64 * k_row_bytes, vs64 = 64 * v_row_bytes;
+
+  // First item: Q and tiles 0-2 in flight.
+  load_q(cur);
+  issue_tile(0);
+  issue_tile(1);
+  issue_tile(2);
+
+  for (;;) {
+    // segment bounds of the next round's item, loaded now (lane 0: start,
+    // lane 1: end) so they have arrived when this item ends
+    const int kc = k + 1, ic = item_index(kc);
+    const bool cand = kc * P < n_items && ic < n_items;
+    const int c_sg = (cand ? seg_of(ic) : 0) + (lane & 1);
+    const int c_q = a.cu_q[c_sg];
+    const int c_k = a.cu_k[c_sg];
+
+    const int qi = cur.qb * BQ + wq * 32 + col;
+    const int shift = cur.Lk - cur.Lq;
+    const int w_qmin = cur.qb * BQ + wq * 32;
+    const int w_qmax = min(w_qmin + 31, cur.Lq - 1);
+    const int w_end = w_qmin >= cur.Lq ? 0 : (CAUSAL ? max(0, min(cur.Lk, w_qmax + 1 + shift)) : cur.Lk);
+    const int w_full = CAUSAL ? max(0, min(cur.Lk, w_qmin + 1 + shift)) : cur.Lk;  // keys < w_full: no mask
+    const int my_lim = CAUSAL ? min(cur.Lk, qi + 1 + shift) : cur.Lk;
+    const int nt = (kv_end + BKV - 1) / BKV;  // LDS tiles (workgroup-uniform)
+    const int nsub = (w_end + 31) / 32;       // 32-key sub-tiles of this wave
+
+    // tile 0 has landed for every wave (tiles 1, 2 may be in flight)
+    wait_tiles(2);
+    barrier();
+    // The item: O = softmax(Q K^T) V for both columns, normalised and
+    // written to this wave's LDS staging rows (see gen_prefill_wide_asm.py).
+    {
+      int r_t, r_j, r0, r1, r2, r3, r4, r5, r6;
+      unsigned long long r_ret;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+      asm volatile(AAC_PW_ITEM_ASM
+                   : [t] "=&s"(r_t), [j] "=&s"(r_j), [s0] "=&s"(r0), [s1] "=&s"(r1), [s2] "=&s"(r2),
+                     [s3] "=&s"(r3), [s4] "=&s"(r4), [s5] "=&s"(r5), [s6] "=&s"(r6), [ret] "=&s"(r_ret)
+                   : [q00] "v"(qf[0][0]), [q01] "v"(qf[0][1]), [q02] "v"(qf[0][2]), [q03] "v"(qf[0][3]),
+                     [q04] "v"(qf[0][4]), [q05] "v"(qf[0][5]), [q06] "v"(qf[0][6]), [q07] "v"(qf[0][7]),
+                     [q10] "v"(qf[1][0]), [q11] "v"(qf[1][1]), [q12] "v"(qf[1][2]), [q13] "v"(qf[1][3]),
+                     [q14] "v"(qf[1][4]), [q15] "v"(qf[1][5]), [q16] "v"(qf[1][6]), [q17] "v"(qf[1][7]),
+                     [ko0] "v"(koff[0]), [ko1] "v"(koff[1]), [ko2] "v"(koff[2]), [ko3] "v"(koff[3]),
+                     [ko4] "v"(koff[4]), [ko5] "v"(koff[5]), [ko6] "v"(koff[6]), [ko7] "v"(koff[7]),
+                     [vo0] "v"(voff[0]), [vo1] "v"(voff[1]), [vo2] "v"(voff[2]), [vo3] "v"(voff[3]),
+                     [sel] "v"(sel), [cs] "s"(cs), [ncs] "s"(ncs), [kthr] "s"(kthr), [mylim] "v"(my_lim),
+                     [hl4] "v"(hl4), [bpa] "v"(bpa), [bpahi] "v"(bpahi), [hi16] "v"(hi16),
+                     [obase] "v"(obase), [lds0] "s"(lds0), [ldsw] "s"(ldsw), [rsk] "s"(rsk), [rsv] "s"(rsv),
+                     [ldk] "v"(ld_voff_k), [ldv] "v"(ld_voff_v), [ks16] "s"(ks16), [vs16] "s"(vs16),
+                     [ks64] "s"(ks64), [vs64] "s"(vs64), [nsub] "s"(nsub), [wfull] "s"(w_full), [nt] "s"(nt)
+                   : AAC_PW_CLOBBERS);
+#pragma clang diagnostic pop
+    }
+
+    // The next item (its Q loads go out once this item's are dead).
+    Item nxt;
+    int kn = kc;
+    bool more;
+    if (cand && decode(ic, __builtin_amdgcn_readlane(c_q, 0), __builtin_amdgcn_readlane(c_q, 1),
+                       __builtin_amdgcn_readlane(c_k, 0), __builtin_amdgcn_readlane(c_k, 1), nxt)) {
+      more = true;
+    } else {
+      kn = kc + 1;
+      more = kc * P < n_items && next_item(kn, nxt);
+    }
+    if (more) load_q(nxt);
+    // ---- store: each store instruction writes four whole 256-byte head rows
+    const u16* const ldsw16 = reinterpret_cast<const u16*>(lds);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const u16* ob = ldsw16 + (wave * 2 + c) * (32 * OPITCH);
+      constexpr int kNt = 2;  // non-temporal stores
+      const int row0 = cur.qb * BQ + wq * 32;
+      const int nrow = min(32, cur.Lq - row0);
+      u16* og = a.out + (int64_t)(cur.q_beg + row0) * a.o_stride + (cur.h * G + 2 * wp + c) * D;
+      const int ostep = (int)(a.o_stride * 2);
+      const __amdgpu_buffer_rsrc_t ors =
+          __builtin_amdgcn_make_buffer_rsrc(og, 0, nrow > 0 ? nrow * ostep : 0, 0x00020000);
+      u32x4 val[8];
+#pragma unroll
+      for (int it = 0; it < 8; ++it)
+        val[it] = *reinterpret_cast<const u32x4*>(ob + (4 * it + (lane >> 4)) * OPITCH + (lane & 15) * 8);
+      const int voff_o = (lane >> 4) * ostep + (lane & 15) * 16;
+#pragma unroll
+      for (int it = 0; it < 8; ++it)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val[it]), ors, voff_o,
+                                               4 * it * ostep, kNt);
+    }
+    if (!more) break;
+    __syncthreads();  // output rows read back before the next item's tiles land
+    cur = nxt;
+    k = kn;
+    kv_end = kv_end_of(cur);
+    set_rsrc(cur);
+    issue_tile(0);
+    issue_tile(1);
+    issue_tile(2);
+  }
+}
+
+template <int G, bool CAUSAL, bool F16>
+static void launch_t(const Args& a0, int max_q, int n_cu, hipStream_t st) {
+  Args a = a0;
+  constexpr int BQ = 32 * (kWaves / (G / 2));
+  a.n_qblocks = (int)cdiv(max_q, BQ);
+  const int64_t n_items = (int64_t)a.hkv * a.n_seqs * a.n_qblocks;
+  const int grid = (int)std::min<int64_t>(n_items, n_cu);
+  hipLaunchKernelGGL((prefill_wide_kernel<G, CAUSAL, F16>), dim3(grid), dim3(kThreads), 0, st, a);
+}
+
+template <bool CAUSAL, bool F16>
+static int launch_g(const Args& a, int g, int max_q, int n_cu, hipStream_t st) {
+  switch (g) {
+    case 2: launch_t<2, CAUSAL, F16>(a, max_q, n_cu, st); break;
+    case 4: launch_t<4, CAUSAL, F16>(a, max_q, n_cu, st); break;
+    case 8: launch_t<8, CAUSAL, F16>(a, max_q, n_cu, st); break;
+    default: return AAC_ERR_UNSUPPORTED;
+  }
+  return AAC_OK;
+}
+
+}  // namespace pw
+
+bool prefill_wide_supports(int g, float scale, bool f16) {
+  return (g == 2 || g == 4 || g == 8) && scale > 0.f && !f16;
+}
+
+int prefill_wide_launch(const pf::Args& a, int g, bool causal, int max_q, int n_cu, hipStream_t st) {
+  return causal ? pw::launch_g<true, false>(a, g, max_q, n_cu, st)
+                : pw::launch_g<false, false>(a, g, max_q, n_cu, st);
+}
+
+}  // namespace aac

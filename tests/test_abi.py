@@ -145,3 +145,14 @@ def test_header_compiles_as_c_and_links(tmp_path):
     assert r.returncode == 0, r.stdout + r.stderr
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout + r.stderr
+
+
+def test_generated_prefill_assembly_matches_its_generator():
+    """csrc/prefill_wide_asm.inc is written by csrc/gen_prefill_wide_asm.py;
+    the committed file must be exactly what the generator prints, so a change
+    to either one cannot drift from the other."""
+    import subprocess
+    import sys
+    gen = Path(__file__).resolve().parent.parent / "awesome_acceleration_amd" / "csrc" / "gen_prefill_wide_asm.py"
+    r = subprocess.run([sys.executable, str(gen), "--check"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
