@@ -201,32 +201,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(Args a) {
   // before cu[0] and from cu[n] on.  Every token's rows are thus written at
   // least once; a row written twice gets the same bytes both times.  The
   // store's arguments are read from the kernel-argument segment where they
-  // are used (the empty asm hides the pointer's origin), so they hold no
-  // SGPRs through the tile loop.
-  typedef const Args __attribute__((address_space(4))) KArgs;
-  auto sargs = [&]() {
-    KArgs* p = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-    asm volatile("" : "+s"(p));
-    return p;
-  };
+  // are used, so they hold no SGPRs through the tile loop.
+  auto sargs = [&]() { return kernel_args(); };
   auto copy_span = [&](int64_t t0, int64_t t1, int h0, int h1) {  // the rare paths
-    KArgs* sa = sargs();
-    t0 = max(t0, (int64_t)0);
-    t1 = min(t1, (int64_t)sa->n_tok);
-    const int nh = h1 - h0;
-    const int64_t n = t1 > t0 ? (t1 - t0) * nh : 0;
-    for (int64_t r = tid >> 4; r < n; r += kThreads / 16) {
-      const int64_t tok = t0 + r / nh;
-      const int hh = h0 + (int)(r % nh);
-      const int64_t sl = sa->slots[tok];
-      const u32x4 kx = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + hh * D + (tid & 15) * 8);
-      const u32x4 vx = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + hh * D + (tid & 15) * 8);
-      if ((uint64_t)sl < (uint64_t)sa->num_rows) {
-        const int64_t dst = (sl * a.hkv + hh) * D + (tid & 15) * 8;
-        *reinterpret_cast<u32x4*>(sa->kc + dst) = kx;
-        *reinterpret_cast<u32x4*>(sa->vc + dst) = vx;
-      }
-    }
+    store_kv_span<kThreads>(a, tid, t0, t1, h0, h1);
   };
   // own rows of an item: thread rows (tid >> 4) + 32 i, 16 B at dim 8 (tid & 15);
   // rows past the q-block repeat its last row (same bytes to the same slot)
@@ -832,11 +810,11 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
                        : pf::launch_g<true, false, false, true>(a, g, max_seqlen_q, n_cu, stream))
                 : (f16 ? pf::launch_g<false, true, false, true>(a, g, max_seqlen_q, n_cu, stream)
                        : pf::launch_g<false, false, false, true>(a, g, max_seqlen_q, n_cu, stream));
-  } else if (n_store > 0)  // the store variant exists for causal attention only
+  } else if (prefill_wide_supports(g, scale, f16))
+    rc = prefill_wide_launch(a, g, causal != 0, n_store > 0, max_seqlen_q, n_cu, stream);
+  else if (n_store > 0)  // the store variant exists for causal attention only
     rc = f16 ? pf::launch_g<true, true, true>(a, g, max_seqlen_q, n_cu, stream)
              : pf::launch_g<true, false, true>(a, g, max_seqlen_q, n_cu, stream);
-  else if (prefill_wide_supports(g, scale, f16))
-    rc = prefill_wide_launch(a, g, causal != 0, max_seqlen_q, n_cu, stream);
   else if (causal)
     rc = f16 ? pf::launch_g<true, true>(a, g, max_seqlen_q, n_cu, stream)
              : pf::launch_g<true, false>(a, g, max_seqlen_q, n_cu, stream);

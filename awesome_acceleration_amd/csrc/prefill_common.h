@@ -98,5 +98,42 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
+// The kernel's arguments read from the kernel-argument segment where they are
+// used: the empty asm hides the pointer's origin, so the compiler keeps none
+// of the fields in SGPRs through the tile loop (the store's fields are needed
+// only after it).
+typedef const Args __attribute__((address_space(4))) KArgs;
+__device__ __forceinline__ KArgs* kernel_args() {
+  KArgs* p = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return p;
+}
+
+// KV-cache store of tokens [t0, t1) (clamped to the n_tok stored tokens) for
+// KV heads [h0, h1): token t's K and V rows to cache row slots[t] (rows with a
+// slot outside [0, num_rows) are skipped).  16 threads per 256-byte row, NT
+// threads of the workgroup take NT / 16 rows per pass.
+template <int NT>
+__device__ __forceinline__ void store_kv_span(const Args& a, int tid, int64_t t0, int64_t t1, int h0,
+                                              int h1) {
+  KArgs* sa = kernel_args();
+  t0 = max(t0, (int64_t)0);
+  t1 = min(t1, (int64_t)sa->n_tok);
+  const int nh = h1 - h0;
+  const int64_t n = t1 > t0 ? (t1 - t0) * nh : 0;
+  for (int64_t r = tid >> 4; r < n; r += NT / 16) {
+    const int64_t tok = t0 + r / nh;
+    const int hh = h0 + (int)(r % nh);
+    const int64_t sl = sa->slots[tok];
+    const u32x4 kx = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + hh * D + (tid & 15) * 8);
+    const u32x4 vx = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + hh * D + (tid & 15) * 8);
+    if ((uint64_t)sl < (uint64_t)sa->num_rows) {
+      const int64_t dst = (sl * a.hkv + hh) * D + (tid & 15) * 8;
+      *reinterpret_cast<u32x4*>(sa->kc + dst) = kx;
+      *reinterpret_cast<u32x4*>(sa->vc + dst) = vx;
+    }
+  }
+}
+
 }  // namespace pf
 }  // namespace aac

@@ -10,7 +10,9 @@ namespace aac {
 bool prefill_wide_supports(int g, float scale, bool f16);
 
 // Launch on the persistent grid (min(items, n_cu) workgroups).  a.n_qblocks
-// is set by the launcher.
-int prefill_wide_launch(const pf::Args& a, int g, bool causal, int max_q, int n_cu, hipStream_t st);
+// is set by the launcher.  store: also write the K/V rows to the KV cache
+// through a.slots (causal self-attention only).
+int prefill_wide_launch(const pf::Args& a, int g, bool causal, bool store, int max_q, int n_cu,
+                        hipStream_t st);
 
 }  // namespace aac

@@ -112,9 +112,10 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, int voff, i
 #pragma clang diagnostic pop
 }
 
-template <int G, bool CAUSAL, bool F16>
+template <int G, bool CAUSAL, bool STORE, bool F16>
 __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
   static_assert(G == 2 || G == 4 || G == 8, "two heads of one KV head per wave");
+  static_assert(CAUSAL || !STORE, "the store variant is causal self-attention");
   constexpr int WP = G / 2;          // head pairs per workgroup
   constexpr int WQ = kWaves / WP;    // 32-query slots per workgroup
   constexpr int BQ = 32 * WQ;
@@ -247,9 +248,61 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
         : "memory");
   };
 
+  // ---- the KV-cache store (STORE).  Each item stores the K/V rows of its own
+  // q-block (its queries' rows taken as keys, since cu_q == cu_k) for its KV
+  // head: loaded right after the item body (the tiles staged them moments
+  // before, so they come from L2) and written after the output.  The item of
+  // rank 0 of a segment also stores the q-blocks no item owns (a max_seqlen_q
+  // below the segment's length), and workgroup 0 the tokens before cu[0] and
+  // from cu[n] on.  Every token's rows are thus written at least once; a row
+  // written twice gets the same bytes both times.
+  constexpr int NP = BQ / 16;  // passes of 16 rows (16 threads per row)
+  int64_t csl[STORE ? NP : 1];
+  u32x4 ck[STORE ? NP : 1], cv[STORE ? NP : 1];
+  auto own_load = [&](const Item& it) {
+    pf::KArgs* sa = pf::kernel_args();
+    const int r0 = it.qb * BQ;
+    const int nr = min(BQ, it.Lq - r0);  // >= 1 for an existing item
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {  // rows past the q-block repeat its last row
+      const int rr = min((tid >> 4) + 16 * p, nr - 1);
+      const int64_t t = (int64_t)it.k_beg + r0 + rr;
+      const int64_t tok = min(t, (int64_t)sa->n_tok - 1);
+      csl[p] = t < sa->n_tok ? sa->slots[tok] : -1;
+      ck[p] = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + it.h * D + (tid & 15) * 8);
+      cv[p] = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + it.h * D + (tid & 15) * 8);
+    }
+  };
+  auto own_store = [&](const Item& it) {
+    pf::KArgs* sa = pf::kernel_args();
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if ((uint64_t)csl[p] < (uint64_t)sa->num_rows) {
+        const int64_t dst = (csl[p] * a.hkv + it.h) * D + (tid & 15) * 8;
+        *reinterpret_cast<u32x4*>(sa->kc + dst) = ck[p];
+        *reinterpret_cast<u32x4*>(sa->vc + dst) = cv[p];
+      }
+    }
+    const int nqb = (it.Lq + BQ - 1) / BQ;
+    if (nqb - 1 - it.qb == 0 && nqb > a.n_qblocks) {  // rank 0 (causal numbering)
+      const int lo = nqb - a.n_qblocks;               // q-blocks [lo, nqb) have items
+      pf::store_kv_span<kThreads>(a, tid, it.k_beg, it.k_beg + (int64_t)lo * BQ, it.h, it.h + 1);
+    }
+  };
+  // workgroup 0: tokens outside [cu[0], cu[n])
+  auto store_edges = [&]() {
+    if (STORE && blockIdx.x == 0) {
+      pf::store_kv_span<kThreads>(a, tid, 0, a.cu_q[0], 0, a.hkv);
+      pf::store_kv_span<kThreads>(a, tid, a.cu_q[a.n_seqs], pf::kernel_args()->n_tok, 0, a.hkv);
+    }
+  };
+
   int k = 0;
   Item cur;
-  if (!next_item(k, cur)) return;
+  if (!next_item(k, cur)) {
+    store_edges();
+    return;
+  }
   int kv_end = kv_end_of(cur);
   __amdgpu_buffer_rsrc_t rsk, rsv;
   auto set_rsrc = [&](const Item& it) {
@@ -352,6 +405,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
 #pragma clang diagnostic pop
     }
 
+    if constexpr (STORE) own_load(cur);
     // The next item (its Q loads go out once this item's are dead).
     Item nxt;
     int kn = kc;
@@ -386,6 +440,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val[it]), ors, voff_o,
                                                4 * it * ostep, kNt);
     }
+    if constexpr (STORE) own_store(cur);
     if (!more) break;
     __syncthreads();  // output rows read back before the next item's tiles land
     cur = nxt;
@@ -396,24 +451,25 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     issue_tile(1);
     issue_tile(2);
   }
+  store_edges();
 }
 
-template <int G, bool CAUSAL, bool F16>
+template <int G, bool CAUSAL, bool STORE, bool F16>
 static void launch_t(const Args& a0, int max_q, int n_cu, hipStream_t st) {
   Args a = a0;
   constexpr int BQ = 32 * (kWaves / (G / 2));
   a.n_qblocks = (int)cdiv(max_q, BQ);
   const int64_t n_items = (int64_t)a.hkv * a.n_seqs * a.n_qblocks;
   const int grid = (int)std::min<int64_t>(n_items, n_cu);
-  hipLaunchKernelGGL((prefill_wide_kernel<G, CAUSAL, F16>), dim3(grid), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL((prefill_wide_kernel<G, CAUSAL, STORE, F16>), dim3(grid), dim3(kThreads), 0, st, a);
 }
 
-template <bool CAUSAL, bool F16>
+template <bool CAUSAL, bool STORE, bool F16>
 static int launch_g(const Args& a, int g, int max_q, int n_cu, hipStream_t st) {
   switch (g) {
-    case 2: launch_t<2, CAUSAL, F16>(a, max_q, n_cu, st); break;
-    case 4: launch_t<4, CAUSAL, F16>(a, max_q, n_cu, st); break;
-    case 8: launch_t<8, CAUSAL, F16>(a, max_q, n_cu, st); break;
+    case 2: launch_t<2, CAUSAL, STORE, F16>(a, max_q, n_cu, st); break;
+    case 4: launch_t<4, CAUSAL, STORE, F16>(a, max_q, n_cu, st); break;
+    case 8: launch_t<8, CAUSAL, STORE, F16>(a, max_q, n_cu, st); break;
     default: return AAC_ERR_UNSUPPORTED;
   }
   return AAC_OK;
@@ -425,9 +481,12 @@ bool prefill_wide_supports(int g, float scale, bool f16) {
   return (g == 2 || g == 4 || g == 8) && scale > 0.f && !f16;
 }
 
-int prefill_wide_launch(const pf::Args& a, int g, bool causal, int max_q, int n_cu, hipStream_t st) {
-  return causal ? pw::launch_g<true, false>(a, g, max_q, n_cu, st)
-                : pw::launch_g<false, false>(a, g, max_q, n_cu, st);
+int prefill_wide_launch(const pf::Args& a, int g, bool causal, bool store, int max_q, int n_cu,
+                        hipStream_t st) {
+  if (store)  // causal self-attention with the KV-cache store
+    return causal ? pw::launch_g<true, true, false>(a, g, max_q, n_cu, st) : AAC_ERR_UNSUPPORTED;
+  return causal ? pw::launch_g<true, false, false>(a, g, max_q, n_cu, st)
+                : pw::launch_g<false, false, false>(a, g, max_q, n_cu, st);
 }
 
 }  // namespace aac
