@@ -2,7 +2,8 @@
 """Generate prefill_wide_asm.inc: the per-item body of the wide prefill kernel
 (prefill_wide.hip) as one gfx950 inline-assembly template.
 
-    python gen_prefill_wide_asm.py        # rewrites prefill_wide_asm.inc
+    python gen_prefill_wide_asm.py           # rewrites prefill_wide_asm.inc
+    python gen_prefill_wide_asm.py --check   # exit 1 if the file is stale
 
 Why assembly.  One wave per SIMD owns two 32-query columns and must keep the
 matrix pipe fed from its own instruction stream.  A hand-ordered slot of
@@ -13,6 +14,24 @@ MFMAs alone on MI355X; the compiler's schedule of the same C++ took ~1100
 name single registers of a compiler-allocated tuple, so the values the
 softmax touches element by element live in fixed registers that the
 statement clobbers; Q, the addressing and the loop bounds are operands.
+
+Schedule.  Sub-tile j (32 keys) runs two slots; slot A(j) issues the MFMAs
+of column 0 and the softmax of column 1, slot B(j) the reverse:
+  A(j): S_0(j+1) = K(j+1) Q_0^T, O_0 += V(j)^T P_0(j) | softmax S_1(j) -> P_1(j)
+        LDS: K(j+2) into K set j%2 (8 x 1 KiB)
+  B(j): S_1(j+1) = K(j+1) Q_1^T, O_1 += V(j)^T P_1(j) | softmax S_0(j+1) -> P_0(j+1)
+        LDS: V(j+1) into V set (j+1)%2 (16 x 512 B)
+so each slot reads 8 KiB from LDS, and with K and V double-buffered no read
+waits on the other column.  Each slot ends with the row max of the scores
+its MFMAs produced and the compare against the rescale threshold; the next
+slot branches on it (not taken unless a row max grew by more than kRescale)
+after its first MFMA, so the compare's latency is hidden.  Tile t (64 keys)
+is iteration t of the loop: a barrier at its start (tile t+1 has landed for
+every wave; no wave still reads tile t-1) and then, when both sub-tiles are
+full and need no causal mask, four slots in straight-line code with the
+eight loads of tile t+3 into the freed stage spread two per slot; otherwise
+a general path with the masks, the wave's last sub-tile and the loads issued
+together.
 
 Register map (fixed, clobbered):
   v152-v167 S0, v168-v183 S1     scores of column 0 / 1 (32 keys x 32 queries)
@@ -27,8 +46,8 @@ Register map (fixed, clobbered):
   v234 NB0 v235 NB1              -M * scale_log2
   v236-v239 T0-T3, v240 NEGINF, v242-v249 scratch (tuples start at even registers)
   a0-a127   O  (column c, dim block db at a[64c+16db : +15])
-  a128-a159 K fragments (8 x 4), a160-a191 V fragments of even sub-tiles,
-  a192-a223 V fragments of odd sub-tiles
+  a128-a159 K set 0, a224-a255 K set 1 (8 x 4 each: one fragment per 16-dim step)
+  a160-a191 V set 0, a192-a223 V set 1 (8 fragments f = 2 db + tt of 4)
 
 Hazards (gfx950), each satisfied by construction below:
   * MFMA result -> VALU read: >= 19 wait states.  Scores are read two or more
@@ -38,9 +57,12 @@ Hazards (gfx950), each satisfied by construction below:
     slot earlier than the P*V MFMAs.
   * Transcendental -> VALU read: 1 wait state (exp results are converted
     three or more instructions later).
-  * An LDS load into a fragment register is issued one MFMA after the last
-    MFMA that reads the register.
+  * An LDS load into a fragment register is issued a slot or more after the
+    last MFMA that reads the register; every MFMA that reads a fragment is
+    preceded by an s_waitcnt lgkmcnt that the read tracker below computes.
   * s_mov m0 -> LDS-DMA load: s_nop 0; VALU write -> v_permlane32_swap: s_nop 1.
+  * VCC holds the compare for the next slot's branch from the end of a slot:
+    nothing between writes VCC except a mask, which compares again.
 """
 from __future__ import annotations
 
@@ -68,7 +90,10 @@ L = [200, 204]
 KA, VA, VB, ZERO = 208, 216, 220, 224
 M, MX, THR, NB = [228, 229], [230, 231], [232, 233], [234, 235]
 T0, T1, T2, T3, NEGINF, SCR = 236, 237, 238, 239, 240, 242
-O_A, KF_A, VF_A = 0, 128, 160
+O_A, VF_A = 0, 160
+KF_SET = [128, 224]
+VGPR_CLOBBER = range(152, 250)
+AGPR_CLOBBER = range(0, 256)
 
 
 def S_t(c):
@@ -95,16 +120,16 @@ def O_t(c, db):
     return ar(O_A + 64 * c + 16 * db, 16)
 
 
-def KF(t):
-    return ar(KF_A + 4 * t, 4)
+def KF(kset, t):  # K fragment of 16-dim step t in set kset
+    return ar(KF_SET[kset] + 4 * t, 4)
 
 
-def VF(par, f):  # V fragment f = 2*db + tt of a sub-tile of parity par
-    return ar(VF_A + 32 * par + 4 * f, 4)
+def VF(vset, f):  # V fragment f = 2*db + tt in set vset
+    return ar(VF_A + 32 * vset + 4 * f, 4)
 
 
-def VF_half(par, f, h):
-    return ar(VF_A + 32 * par + 4 * f + 2 * h, 2)
+def VF_half(vset, f, h):
+    return ar(VF_A + 32 * vset + 4 * f + 2 * h, 2)
 
 
 MFMA = "v_mfma_f32_32x32x16_bf16"
@@ -115,6 +140,7 @@ class Emitter:
     def __init__(self):
         self.lines: list[str] = []
         self.n_label = 0
+        self.stubs: list[str] = []  # out-of-line code, emitted after the body
 
     def __call__(self, s: str):
         self.lines.append(s)
@@ -127,12 +153,57 @@ class Emitter:
         return "\n".join(self.lines)
 
 
+class Lgkm:
+    """In-order LDS read tracker: `pending` lists the tags of the reads in
+    flight, oldest first; need(tag) emits the s_waitcnt that guarantees every
+    read carrying that tag has returned (lgkmcnt counts at most 15)."""
+
+    def __init__(self, pending):
+        self.pending = list(pending)
+
+    def issue(self, tag):
+        self.pending.append(tag)
+
+    def need(self, e, tag):
+        idx = max((i for i, t in enumerate(self.pending) if t == tag), default=-1)
+        if idx < 0:
+            return
+        after = len(self.pending) - idx - 1
+        n = min(after, 15)
+        e(f"s_waitcnt lgkmcnt({n})")
+        self.pending = self.pending[len(self.pending) - n:]
+
+
+# LDS reads of the two slot kinds, in issue order, with the MFMA step each
+# goes after.  A(j): K(j+2), one per even step.  B(j): V(j+1), one half per
+# step, in the order the P*V MFMAs of the next A consume them
+# (step 8 + 4 tt + db uses fragment 2 db + tt).
+K_READ_STEPS = [2 * t for t in range(8)]
+V_ORDER = [(2 * db + tt, h) for tt in range(2) for db in range(4) for h in range(2)]
+
+
+def pv_frag(i):
+    """Fragment (2 db + tt) and accumulator block db of P*V MFMA step i (8-15)."""
+    tt, db = (i - 8) // 4, (i - 8) % 4
+    return 2 * db + tt, db, tt
+
+
+def b_reads_pending():
+    """Pending tags at the start of an A slot: slot B's 16 V halves."""
+    return [("V", f) for f, _ in V_ORDER]
+
+
 def row_max_tail(e, c):
     """MX[c] = max over both lane halves of T0 (the lane-partial max)."""
     e(f"v_mov_b32 {v(T1)}, {v(T0)}")
     e("s_nop 1")
     e(f"v_permlane32_swap_b32 {v(T0)}, {v(T1)}")
     e(f"v_maximum3_f32 {v(MX[c])}, {v(T0)}, {v(T1)}, {v(T1)}")
+
+
+def compare(e, c):
+    """VCC = lanes whose row max passed the rescale threshold of column c."""
+    e(f"v_cmp_gt_f32 vcc, {v(MX[c])}, {v(THR[c])}")
 
 
 def row_max_ops(c):
@@ -163,18 +234,20 @@ def selector(x, tt):
     return f"{SELM} {L_t(x)}, %[sel], {P_t(x, tt)}, {L_t(x)}"
 
 
-def check(e, x):
-    """Rescale column x when some row max exceeds its threshold (rare)."""
-    ok = e.label("Lok")
-    e(f"v_cmp_gt_f32 vcc, {v(MX[x])}, {v(THR[x])}")
-    e(f"s_cbranch_vccz {ok}")
-    e(f"s_call_b64 %[ret], Lresc{x}_%=")
-    e(f"{ok}:")
+def check_branch(e, x):
+    """Rescale column x when the compare left in VCC found a row max past its
+    threshold (rare): a not-taken branch to an out-of-line call."""
+    stub = e.label("Lfix")
+    back = e.label("Lback")
+    e(f"s_cbranch_vccnz {stub}")
+    e(f"{back}:")
+    e.stubs += [f"{stub}:", f"s_call_b64 %[ret], Lresc{x}_%=", f"s_branch {back}"]
 
 
 def mask(e, x, jj_expr_sgpr):
     """Scores of S[x] for keys at or past this lane's limit -> -inf; then the
-    row max MX[x] again.  jj_expr_sgpr holds 32 * (sub-tile index)."""
+    row max MX[x] and its compare again.  jj_expr_sgpr holds 32 * (sub-tile
+    index)."""
     e(f"v_subrev_u32 {v(T2)}, {jj_expr_sgpr}, %[mylim]")
     e(f"v_sub_u32 {v(T2)}, {v(T2)}, %[hl4]")
     for i in range(16):
@@ -184,48 +257,64 @@ def mask(e, x, jj_expr_sgpr):
     for op in row_max_ops(x):
         e(op)
     row_max_tail(e, x)
+    compare(e, x)
 
 
-def slot(e, c, par, kind):
-    """One slot.  c: MFMA column; x = 1 - c: softmax column.
-    kind 'A': no LDS reads; 'B': reload K(j+2) and V(j+1) (par = parity of j).
-    MFMA steps 0-7: S[c] = K Q_c^T; 8-15: O[c] += V^T P[c]."""
+def k_read(kset, t, par):
+    """K fragment t of sub-tile j+2 into set kset; tile t+1, half par."""
+    return f"ds_read_b128 {KF(kset, t)}, {v(KA + t)} offset:{8192 * par}"
+
+
+def v_read(vset, f, h, par):
+    """Half h of V fragment f of sub-tile j+1 into set vset: for par 0 tile t
+    half 1 (VA), for par 1 tile t+1 half 0 (VB)."""
+    base, off0 = (VA, 8192) if par == 0 else (VB, 0)
+    db, tt = f // 2, f % 2
+    return f"ds_read_b64_tr_b16 {VF_half(vset, f, h)}, {v(base + db)} offset:{off0 + 4096 * tt + 2048 * h}"
+
+
+def slot(e, c, par, extra=None):
+    """One slot of sub-tile j (par = j % 2).  c = 0: slot A (MFMA column 0,
+    softmax column 1, reads K(j+2)); c = 1: slot B (MFMA column 1, softmax
+    column 0, reads V(j+1)).  extra: step -> instructions to place after that
+    step's MFMA (the spread tile loads)."""
     x = 1 - c
+    kuse, kset_new = 1 - par, par          # K(j+1) in set (j+1)%2; K(j+2) into set j%2
+    vuse, vset_new = par, 1 - par          # V(j) in set j%2; V(j+1) into set (j+1)%2
     sm = softmax_ops(x)
     mx = row_max_ops(c)
-    reads = [[] for _ in range(17)]
-    if kind == "B":
-        # K(j+2): tile t+1, half par; register t free once MFMA t issued
-        for t in range(8):
-            reads[t + 1].append(f"ds_read_b128 {KF(t)}, {v(KA + t)} offset:{8192 * par}")
-        # V(j+1) into the other parity's registers: par 0 -> tile t half 1 (VA),
-        # par 1 -> tile t+1 half 0 (VB)
-        base, off0 = (VA, 8192) if par == 0 else (VB, 0)
-        vr_list = []
-        for db in range(4):
-            for tt in range(2):
-                f = 2 * db + tt
-                for h in range(2):
-                    vr_list.append(f"ds_read_b64_tr_b16 {VF_half(1 - par, f, h)}, {v(base + db)} "
-                                   f"offset:{off0 + 4096 * tt + 2048 * h}")
-        # 16 V reads over steps 2-15 (two at steps 2 and 3)
-        at = [2, 2, 3, 3] + list(range(4, 16))
-        for r, s in zip(vr_list, at):
-            reads[s].append(r)
+    reads = [[] for _ in range(16)]
+    lg = None
+    if c == 0:
+        lg = Lgkm(b_reads_pending())
+        for t, st in enumerate(K_READ_STEPS):
+            reads[st].append((("K", t), k_read(kset_new, t, par)))
+    else:
+        for st, (f, h) in enumerate(V_ORDER):
+            reads[st].append((("V", f), v_read(vset_new, f, h, par)))
     for i in range(16):
-        if kind == "A" and i == 0:
-            e("s_waitcnt lgkmcnt(9)")   # K fragments of this slot landed
-        if kind == "A" and i == 8:
-            e("s_waitcnt lgkmcnt(0)")   # V fragments landed
         if i < 8:
-            e(f"{MFMA} {S_t(c)}, {KF(i)}, %[q{c}{i}], {'0' if i == 0 else S_t(c)}")
+            if lg is not None and i == 0:
+                # K(j+1) was read in the previous A: pending as the oldest reads
+                lg.pending = [("Kold", 0)] * 8 + lg.pending
+                lg.need(e, ("Kold", 0))
+            e(f"{MFMA} {S_t(c)}, {KF(kuse, i)}, %[q{c}{i}], {'0' if i == 0 else S_t(c)}")
         else:
-            tt, db = (i - 8) // 4, (i - 8) % 4
-            e(f"{MFMA} {O_t(c, db)}, {VF(par, 2 * db + tt)}, {P_t(c, tt)}, {O_t(c, db)}")
+            f, db, tt = pv_frag(i)
+            if lg is not None:
+                lg.need(e, ("V", f))
+            e(f"{MFMA} {O_t(c, db)}, {VF(vuse, f)}, {P_t(c, tt)}, {O_t(c, db)}")
+        if i == 0:
+            check_branch(e, x)
         for op in sm[i]:
             e(op)
-        for op in reads[i]:
+        for tag, op in reads[i]:
             e(op)
+            if lg is not None:
+                lg.issue(tag)
+        if extra and i in extra:
+            for op in extra[i]:
+                e(op)
         if i >= 9:
             e(mx[i - 9])
         if i == 11:
@@ -237,15 +326,19 @@ def slot(e, c, par, kind):
         e(op)
     row_max_tail(e, c)
     e(selector(x, 1))
+    compare(e, c)
 
 
 def last(e, par):
-    """Last sub-tile of the wave: softmax of S1 -> P1, then O0 += V P0 and O1 += V P1."""
+    """Last sub-tile j of the wave (par = j % 2): softmax of S1(j) -> P1(j),
+    then O0 += V(j) P0(j) and O1 += V(j) P1(j)."""
     sm = softmax_ops(1)
     e("s_waitcnt lgkmcnt(0)")
     for i in range(8):
-        tt, db = i // 4, i % 4
-        e(f"{MFMA} {O_t(0, db)}, {VF(par, 2 * db + tt)}, {P_t(0, tt)}, {O_t(0, db)}")
+        f, db, tt = pv_frag(8 + i)
+        e(f"{MFMA} {O_t(0, db)}, {VF(par, f)}, {P_t(0, tt)}, {O_t(0, db)}")
+        if i == 0:
+            check_branch(e, 1)
         for op in sm[i]:
             e(op)
     for i in range(8, 17):
@@ -258,8 +351,8 @@ def last(e, par):
     e(selector(1, 0))
     e(selector(1, 1))
     for i in range(8):
-        tt, db = i // 4, i % 4
-        e(f"{MFMA} {O_t(1, db)}, {VF(par, 2 * db + tt)}, {P_t(1, tt)}, {O_t(1, db)}")
+        f, db, tt = pv_frag(8 + i)
+        e(f"{MFMA} {O_t(1, db)}, {VF(par, f)}, {P_t(1, tt)}, {O_t(1, db)}")
 
 
 def rescale_sub(e, x):
@@ -315,6 +408,27 @@ def softmax_block(e, x):
     e(selector(x, 1))
 
 
+def dma_setup(e):
+    """Scalar state of the loads of tile t+3 into its ring stage ((t+3) % 4):
+    %[dm] the LDS address of this wave's first 1 KiB, %[dk] / %[dv] the byte
+    offsets of the K / V rows."""
+    e("s_add_u32 %[s2], %[t], 3")
+    e("s_and_b32 %[dm], %[s2], 3")
+    e("s_lshl_b32 %[dm], %[dm], 15")
+    e("s_add_u32 %[dm], %[dm], %[ldsw]")
+    e("s_mul_i32 %[dk], %[s2], %[ks64]")
+    e("s_mul_i32 %[dv], %[s2], %[vs64]")
+
+
+def dma_load(kind):
+    """One 1 KiB load of tile t+3 (16 rows of K or V) straight into LDS."""
+    if kind == "K":
+        return ["s_mov_b32 m0, %[dm]", "s_nop 0", "buffer_load_dwordx4 %[ldk], %[rsk], %[dk] offen lds",
+                "s_add_u32 %[dk], %[dk], %[ks16]", "s_add_u32 %[dm], %[dm], 0x1000"]
+    return ["s_mov_b32 m0, %[dm]", "s_nop 0", "buffer_load_dwordx4 %[ldv], %[rsv], %[dv] offen lds",
+            "s_add_u32 %[dv], %[dv], %[vs16]", "s_add_u32 %[dm], %[dm], 0x1000"]
+
+
 def generate() -> str:
     e = Emitter()
     # ---------------------------------------------------------------- entry
@@ -329,26 +443,26 @@ def generate() -> str:
         for db in range(4):
             e(f"{MFMA} {O_t(c, db)}, {vr(ZERO, 4)}, {vr(ZERO, 4)}, 0")
     # ------------------------------------------------------------- prologue
+    # S(0) of both columns from K(0) (set 0); then K(1) into set 1 and V(0)
+    # into V set 0 in the order of slot A's and slot B's reads, so the first
+    # A finds the reads in flight that every later A finds.
     e("s_cmp_eq_u32 %[nsub], 0")
     e("s_cbranch_scc1 Lpro_end_%=")
     for t in range(8):
         e(f"v_add_u32 {v(KA + t)}, %[lds0], %[ko{t}]")
     for t in range(8):
-        e(f"ds_read_b128 {KF(t)}, {v(KA + t)}")
-    e("s_waitcnt lgkmcnt(0)")
-    for t in range(8):
-        e(f"{MFMA} {S_t(0)}, {KF(t)}, %[q0{t}], {'0' if t == 0 else S_t(0)}")
-        e(f"{MFMA} {S_t(1)}, {KF(t)}, %[q1{t}], {'0' if t == 0 else S_t(1)}")
-        if t >= 1:
-            e(f"ds_read_b128 {KF(t - 1)}, {v(KA + t - 1)} offset:8192")
-    e(f"ds_read_b128 {KF(7)}, {v(KA + 7)} offset:8192")
+        e(f"ds_read_b128 {KF(0, t)}, {v(KA + t)}")
     e("s_add_u32 %[s2], %[lds0], 0x4000")
     for db in range(4):
         e(f"v_add_u32 {v(VA + db)}, %[s2], %[vo{db}]")
-    for db in range(4):
-        for tt in range(2):
-            for h in range(2):
-                e(f"ds_read_b64_tr_b16 {VF_half(0, 2 * db + tt, h)}, {v(VA + db)} offset:{4096 * tt + 2048 * h}")
+    e("s_waitcnt lgkmcnt(0)")
+    for t in range(8):
+        e(f"{MFMA} {S_t(0)}, {KF(0, t)}, %[q0{t}], {'0' if t == 0 else S_t(0)}")
+        e(f"{MFMA} {S_t(1)}, {KF(0, t)}, %[q1{t}], {'0' if t == 0 else S_t(1)}")
+        e(f"ds_read_b128 {KF(1, t)}, {v(KA + t)} offset:8192")
+    for f, h in V_ORDER:
+        db, tt = f // 2, f % 2
+        e(f"ds_read_b64_tr_b16 {VF_half(0, f, h)}, {v(VA + db)} offset:{4096 * tt + 2048 * h}")
     e("s_nop 7")
     e("s_nop 7")
     e("s_nop 7")
@@ -366,6 +480,7 @@ def generate() -> str:
     e("Lpro_ref_%=:")
     set_ref(e, 0)
     set_ref(e, 1)
+    compare(e, 1)   # false: the reference max of column 1 is its row max
     softmax_block(e, 0)
     e("Lpro_end_%=:")
     # ------------------------------------------------------------ tile loop
@@ -388,8 +503,31 @@ def generate() -> str:
     e("s_add_u32 %[s2], %[s1], 0x4000")
     for db in range(4):
         e(f"v_add_u32 {v(VB + db)}, %[s2], %[vo{db}]")
+    dma_setup(e)
+    # sync: tile t+1 has landed for every wave, and every wave is done with
+    # tile t-1, whose stage the loads of tile t+3 refill
+    e("s_waitcnt vmcnt(8)")
+    e("s_barrier")
+    # straight-line iteration when sub-tiles 2t, 2t+1 are full and unmasked
+    # (64 t + 96 <= w_full implies 2t + 2 < nsub)
+    e("s_lshl_b32 %[s5], %[t], 6")
+    e("s_add_u32 %[s5], %[s5], 96")
+    e("s_cmp_le_u32 %[s5], %[wfull]")
+    e("s_cbranch_scc0 Lgen_%=")
+    loads = [dma_load("K"), dma_load("K"), dma_load("K"), dma_load("K"),
+             dma_load("V"), dma_load("V"), dma_load("V"), dma_load("V")]
     for sub in range(2):
-        # j = 2t + sub;  s5 = j + 1
+        slot(e, 0, sub, extra={3: loads[4 * sub], 11: loads[4 * sub + 1]})
+        slot(e, 1, sub, extra={3: loads[4 * sub + 2], 11: loads[4 * sub + 3]})
+    e("s_add_u32 %[t], %[t], 1")
+    e("s_branch Ltile_%=")
+    # ---- general iteration: the loads together, then per sub-tile j the
+    # masks, the slots, or the wave's last sub-tile
+    e("Lgen_%=:")
+    for ld in loads:
+        for op in ld:
+            e(op)
+    for sub in range(2):
         e("s_lshl_b32 %[j], %[t], 1")
         if sub:
             e("s_add_u32 %[j], %[j], 1")
@@ -397,73 +535,32 @@ def generate() -> str:
         e("s_lshl_b32 %[s6], %[j], 5")              # 32 j
         e("s_cmp_lt_u32 %[s5], %[nsub]")
         e(f"s_cbranch_scc0 Lnofull{sub}_%=")
-        # ---- full sub-tile: slot A(j)
+        # ---- full sub-tile j: A(j), B(j)
         e("s_add_u32 %[s3], %[s6], 32")
         e("s_cmp_gt_u32 %[s3], %[wfull]")
         e(f"s_cbranch_scc0 LmA{sub}_%=")
         mask(e, 1, "%[s6]")
         e(f"LmA{sub}_%=:")
-        check(e, 1)
-        slot(e, 0, sub, "A")
-        if sub == 0:
-            e(f"s_branch Lsync_%=")
-        else:
-            e(f"s_branch LB{sub}_%=")
-        # ---- last sub-tile of the wave
-        e(f"Lnofull{sub}_%=:")
-        e("s_cmp_eq_u32 %[s5], %[nsub]")
-        e(f"s_cbranch_scc0 Lskip{sub}_%=")
-        e("s_add_u32 %[s3], %[s6], 32")
-        e("s_cmp_gt_u32 %[s3], %[wfull]")
-        e(f"s_cbranch_scc0 LmL{sub}_%=")
-        mask(e, 1, "%[s6]")
-        e(f"LmL{sub}_%=:")
-        check(e, 1)
-        last(e, sub)
-        e(f"Lskip{sub}_%=:")
-        if sub == 0:
-            # ---- sync point of the tile: tile t+1 landed everywhere; the
-            # stage of tile t-1 is free for tile t+3
-            e("Lsync_%=:")
-            e("s_waitcnt vmcnt(8)")
-            e("s_barrier")
-            e("s_add_u32 %[s2], %[t], 3")
-            e("s_and_b32 %[s3], %[s2], 3")
-            e("s_lshl_b32 %[s3], %[s3], 15")
-            e("s_add_u32 %[s3], %[s3], %[ldsw]")
-            e("s_mul_i32 %[s4], %[s2], %[ks64]")
-            e("s_mul_i32 %[s2], %[s2], %[vs64]")
-            for i in range(4):
-                e("s_mov_b32 m0, %[s3]")
-                e("s_nop 0")
-                e("buffer_load_dwordx4 %[ldk], %[rsk], %[s4] offen lds")
-                e("s_add_u32 %[s4], %[s4], %[ks16]")
-                e("s_add_u32 %[s3], %[s3], 0x1000")
-            for i in range(4):
-                e("s_mov_b32 m0, %[s3]")
-                e("s_nop 0")
-                e("buffer_load_dwordx4 %[ldv], %[rsv], %[s2] offen lds")
-                e("s_add_u32 %[s2], %[s2], %[vs16]")
-                e("s_add_u32 %[s3], %[s3], 0x1000")
-            # slot B(2t) when 2t is a full sub-tile
-            e("s_lshl_b32 %[j], %[t], 1")
-            e("s_add_u32 %[s5], %[j], 1")
-            e("s_cmp_lt_u32 %[s5], %[nsub]")
-            e(f"s_cbranch_scc0 LBend{sub}_%=")
-        else:
-            e(f"s_branch LBend{sub}_%=")
-        e(f"LB{sub}_%=:")
-        # ---- slot B(j): mask S0 (sub-tile j+1) when needed
-        e("s_lshl_b32 %[s6], %[j], 5")
+        slot(e, 0, sub)
         e("s_add_u32 %[s3], %[s6], 64")
         e("s_cmp_gt_u32 %[s3], %[wfull]")
         e(f"s_cbranch_scc0 LmB{sub}_%=")
         e("s_add_u32 %[s3], %[s6], 32")
         mask(e, 0, "%[s3]")
         e(f"LmB{sub}_%=:")
-        check(e, 0)
-        slot(e, 1, sub, "B")
-        e(f"LBend{sub}_%=:")
+        slot(e, 1, sub)
+        e(f"s_branch Lsub{sub}_%=")
+        # ---- last sub-tile of the wave
+        e(f"Lnofull{sub}_%=:")
+        e("s_cmp_eq_u32 %[s5], %[nsub]")
+        e(f"s_cbranch_scc0 Lsub{sub}_%=")
+        e("s_add_u32 %[s3], %[s6], 32")
+        e("s_cmp_gt_u32 %[s3], %[wfull]")
+        e(f"s_cbranch_scc0 LmL{sub}_%=")
+        mask(e, 1, "%[s6]")
+        e(f"LmL{sub}_%=:")
+        last(e, sub)
+        e(f"Lsub{sub}_%=:")
     e("s_add_u32 %[t], %[t], 1")
     e("s_branch Ltile_%=")
     e("Ltdone_%=:")
@@ -498,7 +595,9 @@ def generate() -> str:
                 e(f"ds_write_b64 %[obase], {vr(SCR + 4, 2)} offset:{off}")
     e("s_waitcnt lgkmcnt(0)")
     e("s_branch Lend_%=")
-    # ---------------------------------------------------------- subroutines
+    # ------------------------------------------------- out-of-line code
+    for ln in e.stubs:
+        e(ln)
     rescale_sub(e, 0)
     rescale_sub(e, 1)
     e("Lend_%=:")
@@ -509,22 +608,29 @@ HEADER = """// Generated by gen_prefill_wide_asm.py -- do not edit by hand.
 // The per-item body of prefill_wide_kernel (zero-init, scores of sub-tile 0,
 // the tile loop with its slots, masks, rescales and LDS staging, and the
 // normalised output written to the LDS staging area) as one gfx950
-// inline-assembly template; register map and hazard rules in the generator.
+// inline-assembly template, and the registers it clobbers; register map,
+// schedule and hazard rules in the generator.
 #pragma once
 """
 
 
-def main() -> int:
+def render() -> str:
     body = generate()
     lit = "\n".join('  "' + ln.replace('"', '\\"') + '\\n"' for ln in body.split("\n"))
     n = sum(1 for ln in body.split("\n") if ln and not ln.endswith(":"))
-    out = HEADER + f"// {n} instructions.\n#define AAC_PW_ITEM_ASM \\\n" + " \\\n".join(
-        lit.split("\n")) + "\n"
+    clob = ", ".join([f'"v{i}"' for i in VGPR_CLOBBER] + [f'"a{i}"' for i in AGPR_CLOBBER] +
+                     ['"vcc"', '"m0"', '"scc"', '"memory"'])
+    return (HEADER + f"// {n} instructions.\n#define AAC_PW_ITEM_ASM \\\n" + " \\\n".join(lit.split("\n")) +
+            "\n\n#define AAC_PW_CLOBBERS " + clob + "\n")
+
+
+def main() -> int:
+    out = render()
     path = Path(__file__).resolve().parent / "prefill_wide_asm.inc"
     if len(sys.argv) > 1 and sys.argv[1] == "--check":
         return 0 if path.read_text() == out else 1
     path.write_text(out)
-    print(f"wrote {path} ({n} instructions)")
+    print(f"wrote {path}")
     return 0
 
 

@@ -122,13 +122,17 @@ __device__ __forceinline__ void store_kv_span(const Args& a, int tid, int64_t t0
   const int nh = h1 - h0;
   const int64_t n = t1 > t0 ? (t1 - t0) * nh : 0;
   for (int64_t r = tid >> 4; r < n; r += NT / 16) {
+    // the lane's dims, opaque here so that no address is hoisted out of this
+    // rare loop into registers held through the whole kernel
+    int dim = (tid & 15) * 8;
+    asm volatile("" : "+v"(dim));
     const int64_t tok = t0 + r / nh;
     const int hh = h0 + (int)(r % nh);
     const int64_t sl = sa->slots[tok];
-    const u32x4 kx = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + hh * D + (tid & 15) * 8);
-    const u32x4 vx = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + hh * D + (tid & 15) * 8);
+    const u32x4 kx = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + hh * D + dim);
+    const u32x4 vx = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + hh * D + dim);
     if ((uint64_t)sl < (uint64_t)sa->num_rows) {
-      const int64_t dst = (sl * a.hkv + hh) * D + (tid & 15) * 8;
+      const int64_t dst = (sl * a.hkv + hh) * D + dim;
       *reinterpret_cast<u32x4*>(sa->kc + dst) = kx;
       *reinterpret_cast<u32x4*>(sa->vc + dst) = vx;
     }

@@ -56,10 +56,6 @@
 #include "prefill_wide.h"
 #include "prefill_wide_asm.inc"
 
-// Registers the item body keeps its own values in (see gen_prefill_wide_asm.py).
-#define AAC_PW_CLOBBERS \
-  "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159", "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "a0", "a1", "a2", "a3", "a4", "a5", "a6", "a7", "a8", "a9", "a10", "a11", "a12", "a13", "a14", "a15", "a16", "a17", "a18", "a19", "a20", "a21", "a22", "a23", "a24", "a25", "a26", "a27", "a28", "a29", "a30", "a31", "a32", "a33", "a34", "a35", "a36", "a37", "a38", "a39", "a40", "a41", "a42", "a43", "a44", "a45", "a46", "a47", "a48", "a49", "a50", "a51", "a52", "a53", "a54", "a55", "a56", "a57", "a58", "a59", "a60", "a61", "a62", "a63", "a64", "a65", "a66", "a67", "a68", "a69", "a70", "a71", "a72", "a73", "a74", "a75", "a76", "a77", "a78", "a79", "a80", "a81", "a82", "a83", "a84", "a85", "a86", "a87", "a88", "a89", "a90", "a91", "a92", "a93", "a94", "a95", "a96", "a97", "a98", "a99", "a100", "a101", "a102", "a103", "a104", "a105", "a106", "a107", "a108", "a109", "a110", "a111", "a112", "a113", "a114", "a115", "a116", "a117", "a118", "a119", "a120", "a121", "a122", "a123", "a124", "a125", "a126", "a127", "a128", "a129", "a130", "a131", "a132", "a133", "a134", "a135", "a136", "a137", "a138", "a139", "a140", "a141", "a142", "a143", "a144", "a145", "a146", "a147", "a148", "a149", "a150", "a151", "a152", "a153", "a154", "a155", "a156", "a157", "a158", "a159", "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172", "a173", "a174", "a175", "a176", "a177", "a178", "a179", "a180", "a181", "a182", "a183", "a184", "a185", "a186", "a187", "a188", "a189", "a190", "a191", "a192", "a193", "a194", "a195", "a196", "a197", "a198", "a199", "a200", "a201", "a202", "a203", "a204", "a205", "a206", "a207", "a208", "a209", "a210", "a211", "a212", "a213", "a214", "a215", "a216", "a217", "a218", "a219", "a220", "a221", "a222", "a223", "vcc", "m0", "scc", "memory"
-
 namespace aac {
 namespace pw {
 
@@ -76,24 +72,6 @@ constexpr int kTileBytes = BKV * D * 2;    // 16 KiB: one K or V tile
 constexpr int kStageBytes = 2 * kTileBytes;
 constexpr int kLdsBytes = kRing * kStageBytes;  // 128 KiB
 constexpr int kLoadsPerTile = 8;           // direct loads per thread per tile (4 K + 4 V)
-
-template <bool F16> struct Sel;
-// 16x16x32 MFMA for the row sums: A is a constant selector, B the probability
-// fragment of one 16-key step (the B operand of the P*V product).
-template <> struct Sel<false> {
-  __device__ static inline f32x4 run(const u32x4& a, const u32x4& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  static constexpr u32 kOnes = 0x3f803f80u;
-};
-template <> struct Sel<true> {
-  __device__ static inline f32x4 run(const u32x4& a, const u32x4& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  static constexpr u32 kOnes = 0x3c003c00u;
-};
 
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 typedef short v4s __attribute__((ext_vector_type(4)));
@@ -119,8 +97,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
   constexpr int WP = G / 2;          // head pairs per workgroup
   constexpr int WQ = kWaves / WP;    // 32-query slots per workgroup
   constexpr int BQ = 32 * WQ;
-  typedef pf::Mfma<F16> M;
-  typedef Sel<F16> SM;
+  static_assert(!F16, "the item body is written for bf16");
 
   // LDS: kRing stages of [K tile | V tile]; after each item the ring stages
   // the output tile (eight 32-row blocks of padded 256-byte rows).
@@ -161,14 +138,15 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) voff[db] = l0 + 64 * (db ^ (i >> 2));
   }
-  // selector of the row-sum MFMA: A[0][k] = 1 for k in [0,8) u [16,24) (the
+  // selector of the row-sum MFMA (16x16x32, A = selector, B = probabilities
+  // of one 16-key step): A[0][k] = 1 for k in [0,8) u [16,24) (the
   // probabilities of queries 0-15), A[1][k] = 1 for k in [8,16) u [24,32)
   // (queries 16-31); lane l holds A[l%16][8 (l/16) ..+7]
   u32x4 sel;
   {
     const bool one = lane == 0 || lane == 32 || lane == 17 || lane == 49;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sel[i] = one ? SM::kOnes : 0u;
+    for (int i = 0; i < 4; ++i) sel[i] = one ? 0x3f803f80u : 0u;  // bf16 ones
   }
 
   // ---- work items (q-block rank z, segment s, KV head h), rank-major so the
@@ -250,37 +228,38 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
 
   // ---- the KV-cache store (STORE).  Each item stores the K/V rows of its own
   // q-block (its queries' rows taken as keys, since cu_q == cu_k) for its KV
-  // head: loaded right after the item body (the tiles staged them moments
-  // before, so they come from L2) and written after the output.  The item of
-  // rank 0 of a segment also stores the q-blocks no item owns (a max_seqlen_q
-  // below the segment's length), and workgroup 0 the tokens before cu[0] and
-  // from cu[n] on.  Every token's rows are thus written at least once; a row
+  // head after its output (the tiles staged those rows moments before, so
+  // they come from L2), in batches of four 16-row passes.  The item of rank 0
+  // of a segment also stores the q-blocks no item owns (a max_seqlen_q below
+  // the segment's length), and workgroup 0 the tokens before cu[0] and from
+  // cu[n] on.  Every token's rows are thus written at least once; a row
   // written twice gets the same bytes both times.
   constexpr int NP = BQ / 16;  // passes of 16 rows (16 threads per row)
-  int64_t csl[STORE ? NP : 1];
-  u32x4 ck[STORE ? NP : 1], cv[STORE ? NP : 1];
-  auto own_load = [&](const Item& it) {
+  constexpr int NB = NP < 4 ? NP : 4;
+  auto own_store = [&](const Item& it) {
     pf::KArgs* sa = pf::kernel_args();
     const int r0 = it.qb * BQ;
     const int nr = min(BQ, it.Lq - r0);  // >= 1 for an existing item
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {  // rows past the q-block repeat its last row
-      const int rr = min((tid >> 4) + 16 * p, nr - 1);
-      const int64_t t = (int64_t)it.k_beg + r0 + rr;
-      const int64_t tok = min(t, (int64_t)sa->n_tok - 1);
-      csl[p] = t < sa->n_tok ? sa->slots[tok] : -1;
-      ck[p] = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + it.h * D + (tid & 15) * 8);
-      cv[p] = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + it.h * D + (tid & 15) * 8);
-    }
-  };
-  auto own_store = [&](const Item& it) {
-    pf::KArgs* sa = pf::kernel_args();
+    for (int p0 = 0; p0 < NP; p0 += NB) {
+      int64_t csl[NB];
+      u32x4 ck[NB], cv[NB];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      if ((uint64_t)csl[p] < (uint64_t)sa->num_rows) {
-        const int64_t dst = (csl[p] * a.hkv + it.h) * D + (tid & 15) * 8;
-        *reinterpret_cast<u32x4*>(sa->kc + dst) = ck[p];
-        *reinterpret_cast<u32x4*>(sa->vc + dst) = cv[p];
+      for (int i = 0; i < NB; ++i) {  // rows past the q-block repeat its last row
+        const int rr = min((tid >> 4) + 16 * (p0 + i), nr - 1);
+        const int64_t t = (int64_t)it.k_beg + r0 + rr;
+        const int64_t tok = min(t, (int64_t)sa->n_tok - 1);
+        csl[i] = t < sa->n_tok ? sa->slots[tok] : -1;
+        ck[i] = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + it.h * D + (tid & 15) * 8);
+        cv[i] = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + it.h * D + (tid & 15) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        if ((uint64_t)csl[i] < (uint64_t)sa->num_rows) {
+          const int64_t dst = (csl[i] * a.hkv + it.h) * D + (tid & 15) * 8;
+          *reinterpret_cast<u32x4*>(sa->kc + dst) = ck[i];
+          *reinterpret_cast<u32x4*>(sa->vc + dst) = cv[i];
+        }
       }
     }
     const int nqb = (it.Lq + BQ - 1) / BQ;
@@ -371,7 +350,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     const int w_qmin = cur.qb * BQ + wq * 32;
     const int w_qmax = min(w_qmin + 31, cur.Lq - 1);
     const int w_end = w_qmin >= cur.Lq ? 0 : (CAUSAL ? max(0, min(cur.Lk, w_qmax + 1 + shift)) : cur.Lk);
-    const int w_full = CAUSAL ? max(0, min(cur.Lk, w_qmin + 1 + shift)) : cur.Lk;  // keys < w_full: no mask
+    // keys < w_full need no mask (at most w_end: a wave without queries has none)
+    const int w_full = min(w_end, CAUSAL ? max(0, min(cur.Lk, w_qmin + 1 + shift)) : cur.Lk);
     const int my_lim = CAUSAL ? min(cur.Lk, qi + 1 + shift) : cur.Lk;
     const int nt = (kv_end + BKV - 1) / BKV;  // LDS tiles (workgroup-uniform)
     const int nsub = (w_end + 31) / 32;       // 32-key sub-tiles of this wave
@@ -382,13 +362,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     // The item: O = softmax(Q K^T) V for both columns, normalised and
     // written to this wave's LDS staging rows (see gen_prefill_wide_asm.py).
     {
-      int r_t, r_j, r0, r1, r2, r3, r4, r5, r6;
+      int r_t, r_j, r0, r1, r2, r3, r5, r6, r_dm, r_dk, r_dv;
       unsigned long long r_ret;
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
       asm volatile(AAC_PW_ITEM_ASM
                    : [t] "=&s"(r_t), [j] "=&s"(r_j), [s0] "=&s"(r0), [s1] "=&s"(r1), [s2] "=&s"(r2),
-                     [s3] "=&s"(r3), [s4] "=&s"(r4), [s5] "=&s"(r5), [s6] "=&s"(r6), [ret] "=&s"(r_ret)
+                     [s3] "=&s"(r3), [s5] "=&s"(r5), [s6] "=&s"(r6), [dm] "=&s"(r_dm), [dk] "=&s"(r_dk),
+                     [dv] "=&s"(r_dv), [ret] "=&s"(r_ret)
                    : [q00] "v"(qf[0][0]), [q01] "v"(qf[0][1]), [q02] "v"(qf[0][2]), [q03] "v"(qf[0][3]),
                      [q04] "v"(qf[0][4]), [q05] "v"(qf[0][5]), [q06] "v"(qf[0][6]), [q07] "v"(qf[0][7]),
                      [q10] "v"(qf[1][0]), [q11] "v"(qf[1][1]), [q12] "v"(qf[1][2]), [q13] "v"(qf[1][3]),
@@ -405,7 +386,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
 #pragma clang diagnostic pop
     }
 
-    if constexpr (STORE) own_load(cur);
     // The next item (its Q loads go out once this item's are dead).
     Item nxt;
     int kn = kc;
