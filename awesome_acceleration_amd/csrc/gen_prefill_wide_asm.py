@@ -132,6 +132,15 @@ def VF_half(vset, f, h):
     return ar(VF_A + 32 * vset + 4 * f + 2 * h, 2)
 
 
+# Schedule options (kept switchable so the slot can be timed in isolation):
+# LAYOUT places the softmax ops over the MFMA steps ("base": op i of each
+# kind at step i / i+1, the last exp and convert after step 15; "early2": two
+# elements at step 0 and one ahead after, all done by step 15).  PARTIAL
+# compares the lane-partial row max with the threshold (any lane over it
+# rescales; only the rescale needs the cross-half max).
+LAYOUT = "early2"
+PARTIAL = True
+
 MFMA = "v_mfma_f32_32x32x16_bf16"
 SELM = "v_mfma_f32_16x16x32_bf16"
 
@@ -179,6 +188,7 @@ class Lgkm:
 # step, in the order the P*V MFMAs of the next A consume them
 # (step 8 + 4 tt + db uses fragment 2 db + tt).
 K_READ_STEPS = [2 * t for t in range(8)]
+V_READ_STEPS = list(range(16))
 V_ORDER = [(2 * db + tt, h) for tt in range(2) for db in range(4) for h in range(2)]
 
 
@@ -206,6 +216,11 @@ def compare(e, c):
     e(f"v_cmp_gt_f32 vcc, {v(MX[c])}, {v(THR[c])}")
 
 
+def compare_partial(e, c):
+    """VCC = lanes whose partial row max (T0) passed the threshold of column c."""
+    e(f"v_cmp_gt_f32 vcc, {v(T0)}, {v(THR[c])}")
+
+
 def row_max_ops(c):
     """The lane-partial max of S[c] as 8 instructions (T0)."""
     ops = [f"v_maximum3_f32 {v(T0)}, {S_e(c, 0)}, {S_e(c, 1)}, {S_e(c, 2)}"]
@@ -217,17 +232,37 @@ def row_max_ops(c):
 
 def softmax_ops(x):
     """Per-step VALU of the softmax of S[x] in place -> P[x]: entries 0-15 go
-    beside MFMA steps 0-15, entry 16 (the last exp) and entry 17 (the last
-    convert) after them, with at least one instruction between the two."""
+    beside MFMA steps 0-15, entries 16 and 17 after them.  A convert reads
+    exp results of an earlier entry (one instruction at least between a
+    transcendental and its reader)."""
     steps = [[] for _ in range(18)]
-    for i in range(16):
-        steps[i].append(f"v_fma_f32 {S_e(x, i)}, {S_e(x, i)}, %[cs], {v(NB[x])}")
-    for i in range(16):
-        steps[i + 1].append(f"v_exp_f32 {S_e(x, i)}, {S_e(x, i)}")
-    for w in range(8):
-        at = 2 * w + 3 if w < 7 else 17
-        steps[at].append(f"v_cvt_pk_bf16_f32 {P_e(x, w)}, {S_e(x, 2 * w)}, {S_e(x, 2 * w + 1)}")
+    fma = lambda i: f"v_fma_f32 {S_e(x, i)}, {S_e(x, i)}, %[cs], {v(NB[x])}"
+    ex = lambda i: f"v_exp_f32 {S_e(x, i)}, {S_e(x, i)}"
+    cvt = lambda w: f"v_cvt_pk_bf16_f32 {P_e(x, w)}, {S_e(x, 2 * w)}, {S_e(x, 2 * w + 1)}"
+    if LAYOUT == "base":
+        for i in range(16):
+            steps[i].append(fma(i))
+        for i in range(16):
+            steps[i + 1].append(ex(i))
+        for w in range(8):
+            steps[2 * w + 3 if w < 7 else 17].append(cvt(w))
+    elif LAYOUT == "early2":
+        steps[0] += [fma(0), fma(1), ex(0), ex(1)]
+        for st in range(1, 15):
+            steps[st].append(fma(st + 1))
+            if st % 2 == 1:
+                steps[st].append(cvt((st - 1) // 2))
+            steps[st].append(ex(st + 1))
+        steps[15].append(cvt(7))
+    else:
+        raise ValueError(LAYOUT)
     return steps
+
+
+def sel0_step():
+    """Step after whose MFMA the first row-sum MFMA goes (two instructions or
+    more after the convert of the last word of P[x](0))."""
+    return 11 if LAYOUT == "base" else 9
 
 
 def selector(x, tt):
@@ -244,10 +279,11 @@ def check_branch(e, x):
     e.stubs += [f"{stub}:", f"s_call_b64 %[ret], Lresc{x}_%=", f"s_branch {back}"]
 
 
-def mask(e, x, jj_expr_sgpr):
+def mask(e, x, jj_expr_sgpr, full=False):
     """Scores of S[x] for keys at or past this lane's limit -> -inf; then the
-    row max MX[x] and its compare again.  jj_expr_sgpr holds 32 * (sub-tile
-    index)."""
+    row max and its compare again (with PARTIAL the lane-partial max in T0,
+    the full max MX[x] only when `full`: the prologue's reference max needs
+    it).  jj_expr_sgpr holds 32 * (sub-tile index)."""
     e(f"v_subrev_u32 {v(T2)}, {jj_expr_sgpr}, %[mylim]")
     e(f"v_sub_u32 {v(T2)}, {v(T2)}, %[hl4]")
     for i in range(16):
@@ -256,8 +292,11 @@ def mask(e, x, jj_expr_sgpr):
         e(f"v_cndmask_b32 {S_e(x, i)}, {v(NEGINF)}, {S_e(x, i)}, vcc")
     for op in row_max_ops(x):
         e(op)
-    row_max_tail(e, x)
-    compare(e, x)
+    if PARTIAL and not full:
+        compare_partial(e, x)
+    else:
+        row_max_tail(e, x)
+        compare(e, x)
 
 
 def k_read(kset, t, par):
@@ -290,7 +329,7 @@ def slot(e, c, par, extra=None):
         for t, st in enumerate(K_READ_STEPS):
             reads[st].append((("K", t), k_read(kset_new, t, par)))
     else:
-        for st, (f, h) in enumerate(V_ORDER):
+        for st, (f, h) in zip(V_READ_STEPS, V_ORDER):
             reads[st].append((("V", f), v_read(vset_new, f, h, par)))
     for i in range(16):
         if i < 8:
@@ -317,16 +356,21 @@ def slot(e, c, par, extra=None):
                 e(op)
         if i >= 9:
             e(mx[i - 9])
-        if i == 11:
+        if i == sel0_step():
             e(selector(x, 0))
     for op in sm[16]:
         e(op)
     e(mx[7])
     for op in sm[17]:
         e(op)
-    row_max_tail(e, c)
-    e(selector(x, 1))
-    compare(e, c)
+    if PARTIAL:
+        compare_partial(e, c)
+        e("s_nop 0")
+        e(selector(x, 1))
+    else:
+        row_max_tail(e, c)
+        e(selector(x, 1))
+        compare(e, c)
 
 
 def last(e, par):
@@ -341,12 +385,10 @@ def last(e, par):
             check_branch(e, 1)
         for op in sm[i]:
             e(op)
-    for i in range(8, 17):
+    for i in range(8, 18):
+        e("s_nop 0")
         for op in sm[i]:
             e(op)
-    e("s_nop 0")
-    for op in sm[17]:
-        e(op)
     e("s_nop 1")
     e(selector(1, 0))
     e(selector(1, 1))
@@ -362,6 +404,8 @@ def rescale_sub(e, x):
     e("s_nop 7")
     e("s_nop 7")
     e("s_nop 7")
+    if PARTIAL:
+        row_max_tail(e, x)
     e(f"v_max_f32 {v(T0)}, {v(M[x])}, {v(MX[x])}")
     e(f"v_sub_f32 {v(T1)}, {v(M[x])}, {v(T0)}")
     e(f"v_mul_f32 {v(T1)}, %[cs], {v(T1)}")
@@ -397,12 +441,11 @@ def set_ref(e, x):
 def softmax_block(e, x):
     """The softmax of S[x] with no MFMA beside it (prologue)."""
     sm = softmax_ops(x)
-    for i in range(17):
+    for i in range(18):
+        if i:
+            e("s_nop 0")
         for op in sm[i]:
             e(op)
-    e("s_nop 0")
-    for op in sm[17]:
-        e(op)
     e("s_nop 1")
     e(selector(x, 0))
     e(selector(x, 1))
@@ -469,8 +512,8 @@ def generate() -> str:
     e("s_cmp_lt_u32 %[wfull], 32")
     e("s_cbranch_scc0 Lpro_nomask_%=")
     e("s_mov_b32 %[s6], 0")
-    mask(e, 0, "%[s6]")
-    mask(e, 1, "%[s6]")
+    mask(e, 0, "%[s6]", full=True)
+    mask(e, 1, "%[s6]", full=True)
     e("s_branch Lpro_ref_%=")
     e("Lpro_nomask_%=:")
     for c in range(2):
