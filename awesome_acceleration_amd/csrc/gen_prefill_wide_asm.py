@@ -69,7 +69,6 @@ from __future__ import annotations
 import sys
 from pathlib import Path
 
-OPITCH_BYTES = 136 * 2  # output staging row pitch (bytes), as prefill_common.h OPITCH
 
 
 def v(n):
@@ -91,6 +90,12 @@ KA, VA, VB, ZERO = 208, 216, 220, 224
 M, MX, THR, NB = [228, 229], [230, 231], [232, 233], [234, 235]
 T0, T1, T2, T3, NEGINF, SCR = 236, 237, 238, 239, 240, 242
 O_A, VF_A = 0, 160
+# Buffer resources built in fixed SGPRs (the statement clobbers them): the
+# active K / V sources of the tile loads (this item's, then the next item's
+# from the position where its tiles start), the next item's, and at the end
+# the output rows of this wave.
+RK, RV, RKN, RVN = "s[88:91]", "s[92:95]", "s[80:83]", "s[84:87]"
+SGPR_CLOBBER = range(80, 96)
 KF_SET = [128, 224]
 VGPR_CLOBBER = range(152, 250)
 AGPR_CLOBBER = range(0, 256)
@@ -452,30 +457,60 @@ def softmax_block(e, x):
 
 
 def dma_setup(e):
-    """Scalar state of the loads of tile t+3 into its ring stage ((t+3) % 4):
-    %[dm] the LDS address of this wave's first 1 KiB, %[dk] / %[dv] the byte
-    offsets of the K / V rows."""
+    """Scalar state of the loads of stream position p = t+3 into its ring
+    stage ((g0 + p) % 4): %[dm] the LDS address of this wave's first 1 KiB,
+    %[dk] / %[dv] the byte offsets of the K / V rows.  Positions from nt on
+    are the next item's tiles p - nt (its resources replace this item's)."""
     e("s_add_u32 %[s2], %[t], 3")
-    e("s_and_b32 %[dm], %[s2], 3")
-    e("s_lshl_b32 %[dm], %[dm], 15")
-    e("s_add_u32 %[dm], %[dm], %[ldsw]")
-    e("s_mul_i32 %[dk], %[s2], %[ks64]")
-    e("s_mul_i32 %[dv], %[s2], %[vs64]")
+    e("s_sub_u32 %[s3], %[s2], %[nt]")
+    e("s_cmp_ge_u32 %[s2], %[nt]")
+    e("s_cselect_b32 %[s3], %[s3], %[s2]")
+    e("s_cselect_b64 s[88:89], s[80:81], s[88:89]")
+    e("s_cselect_b64 s[90:91], s[82:83], s[90:91]")
+    e("s_cselect_b64 s[92:93], s[84:85], s[92:93]")
+    e("s_cselect_b64 s[94:95], s[86:87], s[94:95]")
+    e("s_mul_i32 %[dk], %[s3], %[ks64]")
+    e("s_mul_i32 %[dv], %[s3], %[vs64]")
+    stage_addr(e, "%[dm]", "%[s2]", "%[ldsw]")
 
 
-def dma_load(kind):
-    """One 1 KiB load of tile t+3 (16 rows of K or V) straight into LDS."""
+def stage_addr(e, dst, pos, base):
+    """dst = base + 32 KiB * ((g0 + pos) % 4)."""
+    e(f"s_add_u32 {dst}, {pos}, %[g0]")
+    e(f"s_and_b32 {dst}, {dst}, 3")
+    e(f"s_lshl_b32 {dst}, {dst}, 15")
+    e(f"s_add_u32 {dst}, {dst}, {base}")
+
+
+def dma_load(kind, rk=RK, rv=RV):
+    """One 1 KiB load (16 rows of K or V) straight into LDS."""
     if kind == "K":
-        return ["s_mov_b32 m0, %[dm]", "s_nop 0", "buffer_load_dwordx4 %[ldk], %[rsk], %[dk] offen lds",
+        return ["s_mov_b32 m0, %[dm]", "s_nop 0", f"buffer_load_dwordx4 %[ldk], {rk}, %[dk] offen lds",
                 "s_add_u32 %[dk], %[dk], %[ks16]", "s_add_u32 %[dm], %[dm], 0x1000"]
-    return ["s_mov_b32 m0, %[dm]", "s_nop 0", "buffer_load_dwordx4 %[ldv], %[rsv], %[dv] offen lds",
+    return ["s_mov_b32 m0, %[dm]", "s_nop 0", f"buffer_load_dwordx4 %[ldv], {rv}, %[dv] offen lds",
             "s_add_u32 %[dv], %[dv], %[vs16]", "s_add_u32 %[dm], %[dm], 0x1000"]
+
+
+def build_rsrc(e, fixed_lo, base, rng):
+    """Fixed SGPRs fixed_lo..+3 = raw buffer resource {base, rng bytes}."""
+    e(f"s_mov_b64 s[{fixed_lo}:{fixed_lo + 1}], {base}")
+    e(f"s_mov_b32 s{fixed_lo + 2}, {rng}")
+    e(f"s_mov_b32 s{fixed_lo + 3}, 0x20000")
 
 
 def generate() -> str:
     e = Emitter()
     # ---------------------------------------------------------------- entry
+    # This item's Q and first tiles were loaded before the previous item's 32
+    # output stores (the youngest memory operations): once at most 32 are in
+    # flight they have landed; the barrier makes that true for every wave.
+    e("s_waitcnt vmcnt(32)")
     e("s_waitcnt lgkmcnt(0)")
+    build_rsrc(e, 88, "%[kb]", "%[kr]")
+    build_rsrc(e, 92, "%[vb]", "%[vr]")
+    build_rsrc(e, 80, "%[knb]", "%[knr]")
+    build_rsrc(e, 84, "%[vnb]", "%[vnr]")
+    e("s_barrier")
     for i in range(4):
         e(f"v_mov_b32 {v(ZERO + i)}, 0")
     for i in range(8):
@@ -491,11 +526,13 @@ def generate() -> str:
     # A finds the reads in flight that every later A finds.
     e("s_cmp_eq_u32 %[nsub], 0")
     e("s_cbranch_scc1 Lpro_end_%=")
+    e("s_mov_b32 %[s2], 0")
+    stage_addr(e, "%[s0]", "%[s2]", "%[lds0]")    # stage of tile 0
     for t in range(8):
-        e(f"v_add_u32 {v(KA + t)}, %[lds0], %[ko{t}]")
+        e(f"v_add_u32 {v(KA + t)}, %[s0], %[ko{t}]")
     for t in range(8):
         e(f"ds_read_b128 {KF(0, t)}, {v(KA + t)}")
-    e("s_add_u32 %[s2], %[lds0], 0x4000")
+    e("s_add_u32 %[s2], %[s0], 0x4000")
     for db in range(4):
         e(f"v_add_u32 {v(VA + db)}, %[s2], %[vo{db}]")
     e("s_waitcnt lgkmcnt(0)")
@@ -527,30 +564,38 @@ def generate() -> str:
     softmax_block(e, 0)
     e("Lpro_end_%=:")
     # ------------------------------------------------------------ tile loop
-    e("s_mov_b32 %[t], 0")
-    e("Ltile_%=:")
-    e("s_cmp_ge_u32 %[t], %[nt]")
-    e("s_cbranch_scc1 Ltdone_%=")
-    e("s_and_b32 %[s0], %[t], 3")
-    e("s_lshl_b32 %[s0], %[s0], 15")
-    e("s_add_u32 %[s0], %[s0], %[lds0]")          # stage base of tile t
-    e("s_add_u32 %[s1], %[t], 1")
-    e("s_and_b32 %[s1], %[s1], 3")
-    e("s_lshl_b32 %[s1], %[s1], 15")
-    e("s_add_u32 %[s1], %[s1], %[lds0]")          # stage base of tile t+1
+    # Read addresses at the start of iteration t: KA of tile t+1 (K(2t+2),
+    # K(2t+3) in the A slots), VA of tile t (V(2t+1) in B(2t)), VB of tile t+1
+    # (V(2t+2) in B(2t+1)), each refreshed in a slot that does not read it:
+    # VB in A(2t), VA <- VB in A(2t+1), KA in B(2t+1).  %[s0] holds the V base
+    # of tile t+1 and %[s1] the stage of tile t+2 for those updates.
+    e("s_mov_b32 %[s2], 1")
+    stage_addr(e, "%[s1]", "%[s2]", "%[lds0]")
     for t in range(8):
         e(f"v_add_u32 {v(KA + t)}, %[s1], %[ko{t}]")
-    e("s_add_u32 %[s2], %[s0], 0x4000")
+    e("s_mov_b32 %[s2], 0")
+    stage_addr(e, "%[s0]", "%[s2]", "%[lds0]")
+    e("s_add_u32 %[s0], %[s0], 0x4000")
     for db in range(4):
-        e(f"v_add_u32 {v(VA + db)}, %[s2], %[vo{db}]")
-    e("s_add_u32 %[s2], %[s1], 0x4000")
-    for db in range(4):
-        e(f"v_add_u32 {v(VB + db)}, %[s2], %[vo{db}]")
+        e(f"v_add_u32 {v(VA + db)}, %[s0], %[vo{db}]")
+    e("s_mov_b32 %[t], 0")
+    e("s_cmp_eq_u32 %[nt], 0")
+    e("s_cbranch_scc1 Ltdone_%=")
+    e("Ltile_%=:")
+    e("s_add_u32 %[s2], %[t], 1")
+    stage_addr(e, "%[s0]", "%[s2]", "%[lds0]")
+    e("s_add_u32 %[s0], %[s0], 0x4000")          # V base of tile t+1
+    e("s_add_u32 %[s2], %[t], 2")
+    stage_addr(e, "%[s1]", "%[s2]", "%[lds0]")    # stage of tile t+2
     dma_setup(e)
     # sync: tile t+1 has landed for every wave, and every wave is done with
-    # tile t-1, whose stage the loads of tile t+3 refill
+    # tile t-1, whose stage the loads of position t+3 refill (at t = 0 the
+    # entry's wait and barrier did both)
+    e("s_cmp_eq_u32 %[t], 0")
+    e("s_cbranch_scc1 Lsynced_%=")
     e("s_waitcnt vmcnt(8)")
     e("s_barrier")
+    e("Lsynced_%=:")
     # straight-line iteration when sub-tiles 2t, 2t+1 are full and unmasked
     # (64 t + 96 <= w_full implies 2t + 2 < nsub)
     e("s_lshl_b32 %[s5], %[t], 6")
@@ -559,17 +604,32 @@ def generate() -> str:
     e("s_cbranch_scc0 Lgen_%=")
     loads = [dma_load("K"), dma_load("K"), dma_load("K"), dma_load("K"),
              dma_load("V"), dma_load("V"), dma_load("V"), dma_load("V")]
-    for sub in range(2):
-        slot(e, 0, sub, extra={3: loads[4 * sub], 11: loads[4 * sub + 1]})
-        slot(e, 1, sub, extra={3: loads[4 * sub + 2], 11: loads[4 * sub + 3]})
+    vb_upd = [f"v_add_u32 {v(VB + db)}, %[s0], %[vo{db}]" for db in range(4)]
+    va_upd = [f"v_mov_b32 {v(VA + db)}, {v(VB + db)}" for db in range(4)]
+    ka_upd = [f"v_add_u32 {v(KA + t)}, %[s1], %[ko{t}]" for t in range(8)]
+
+    def extras(ld0, ld1, addr, steps):
+        x = {3: list(ld0), 11: list(ld1)}
+        for st, op in zip(steps, addr):
+            x.setdefault(st, []).append(op)
+        return x
+
+    slot(e, 0, 0, extra=extras(loads[0], loads[1], vb_upd, [1, 5, 9, 13]))
+    slot(e, 1, 0, extra=extras(loads[2], loads[3], [], []))
+    slot(e, 0, 1, extra=extras(loads[4], loads[5], va_upd, [1, 5, 9, 13]))
+    slot(e, 1, 1, extra=extras(loads[6], loads[7], ka_upd, [0, 2, 4, 6, 8, 10, 12, 14]))
     e("s_add_u32 %[t], %[t], 1")
-    e("s_branch Ltile_%=")
+    e("s_cmp_lt_u32 %[t], %[nt]")
+    e("s_cbranch_scc1 Ltile_%=")
+    e("s_branch Ltdone_%=")
     # ---- general iteration: the loads together, then per sub-tile j the
     # masks, the slots, or the wave's last sub-tile
     e("Lgen_%=:")
     for ld in loads:
         for op in ld:
             e(op)
+    for op in vb_upd:
+        e(op)
     for sub in range(2):
         e("s_lshl_b32 %[j], %[t], 1")
         if sub:
@@ -604,16 +664,48 @@ def generate() -> str:
         e(f"LmL{sub}_%=:")
         last(e, sub)
         e(f"Lsub{sub}_%=:")
+    for op in va_upd + ka_upd:
+        e(op)
     e("s_add_u32 %[t], %[t], 1")
-    e("s_branch Ltile_%=")
+    e("s_cmp_lt_u32 %[t], %[nt]")
+    e("s_cbranch_scc1 Ltile_%=")
     e("Ltdone_%=:")
     # ------------------------------------------------------------- epilogue
-    # every wave is done with the ring and no tile load is still writing it
-    e("s_waitcnt vmcnt(0) lgkmcnt(0)")
+    # (1) Items of fewer than three tiles: the next item's tiles at stream
+    # positions nt..2 (its tiles 0..2-nt) go into the stages of this item's
+    # phantom tiles once every wave is done with the ring.
+    e("s_cmp_lt_u32 %[nt], 3")
+    e("s_cbranch_scc0 Lnomiss_%=")
+    e("s_waitcnt lgkmcnt(0)")
     e("s_barrier")
+    e("s_mov_b32 %[s2], %[nt]")
+    e("Lmiss_%=:")
+    e("s_sub_u32 %[s3], %[s2], %[nt]")
+    e("s_mul_i32 %[dk], %[s3], %[ks64]")
+    e("s_mul_i32 %[dv], %[s3], %[vs64]")
+    stage_addr(e, "%[dm]", "%[s2]", "%[ldsw]")
+    for kind in "KKKKVVVV":
+        for op in dma_load(kind, RKN, RVN):
+            e(op)
+    e("s_add_u32 %[s2], %[s2], 1")
+    e("s_cmp_lt_u32 %[s2], 3")
+    e("s_cbranch_scc1 Lmiss_%=")
+    e("Lnomiss_%=:")
+    # (2) Q of the next item into the Q operands (their last reader, the
+    # score MFMAs, issued long ago)
+    for c in range(2):
+        for t in range(8):
+            e(f"global_load_dwordx4 %[q{c}{t}], %[qn], off offset:{256 * c + 32 * t}")
+    # (3) O / l rounded to bf16, through this wave's LDS staging rows (beside
+    # the ring: 32 rows x 128 bytes at a 136-byte pitch, one half of a column
+    # at a time) to whole 128-byte row segments in global memory.  Lane l
+    # holds query l % 32, dims 32 db + 8 i + 4 (l / 32) + 0..3 of register
+    # group i; rows past the segment fall outside the output resource.
+    build_rsrc(e, 88, "%[ob]", "%[orng]")
     e("s_nop 7")
     e("s_nop 7")
     e("s_nop 7")
+    n_pair = 0
     for x in range(2):
         e(f"ds_bpermute_b32 {v(T0)}, %[bpa], {v(L[x])}")
         e(f"ds_bpermute_b32 {v(T1)}, %[bpa], {v(L[x] + 1)}")
@@ -625,18 +717,29 @@ def generate() -> str:
         e(f"v_cndmask_b32 {v(T1)}, 0, {v(T1)}, vcc")              # 1/l, 0 for an empty row
         e("s_nop 1")
         base = O_A + 64 * x
-        for db in range(4):
-            for r in range(4):
-                a0 = base + 16 * db + 4 * r
-                for i in range(4):
-                    e(f"v_accvgpr_read_b32 {v(SCR + i)}, a{a0 + i}")
-                for i in range(4):
-                    e(f"v_mul_f32 {v(SCR + i)}, {v(SCR + i)}, {v(T1)}")
-                e(f"v_cvt_pk_bf16_f32 {v(SCR + 4)}, {v(SCR)}, {v(SCR + 1)}")
-                e(f"v_cvt_pk_bf16_f32 {v(SCR + 5)}, {v(SCR + 2)}, {v(SCR + 3)}")
-                off = x * 32 * OPITCH_BYTES + (32 * db + 8 * r) * 2
-                e(f"ds_write_b64 %[obase], {vr(SCR + 4, 2)} offset:{off}")
-    e("s_waitcnt lgkmcnt(0)")
+        for hh in range(2):
+            for db in (2 * hh, 2 * hh + 1):
+                for r in range(4):
+                    a0 = base + 16 * db + 4 * r
+                    for i in range(4):
+                        e(f"v_accvgpr_read_b32 {v(SCR + i)}, a{a0 + i}")
+                    for i in range(4):
+                        e(f"v_mul_f32 {v(SCR + i)}, {v(SCR + i)}, {v(T1)}")
+                    out = SCR + 4 + 2 * (n_pair % 2)   # alternate pairs between writes
+                    n_pair += 1
+                    e(f"v_cvt_pk_bf16_f32 {v(out)}, {v(SCR)}, {v(SCR + 1)}")
+                    e(f"v_cvt_pk_bf16_f32 {v(out + 1)}, {v(SCR + 2)}, {v(SCR + 3)}")
+                    e(f"ds_write_b64 %[stw], {vr(out, 2)} offset:{64 * (db % 2) + 16 * r}")
+            e("s_waitcnt lgkmcnt(0)")
+            # rows 8 i + l / 8, bytes 16 (l % 8) of the half (the scores' registers are free)
+            for i in range(4):
+                e(f"ds_read_b128 {vr(S[0] + 4 * i, 4)}, %[str] offset:{1088 * i}")
+            e("s_waitcnt lgkmcnt(0)")
+            e("s_mov_b32 %[s2], 0")
+            for i in range(4):
+                e(f"buffer_store_dwordx4 {vr(S[0] + 4 * i, 4)}, %[osv], {RK}, %[s2] offen offset:{256 * x + 128 * hh}")
+                if i < 3:
+                    e("s_add_u32 %[s2], %[s2], %[ost8]")
     e("s_branch Lend_%=")
     # ------------------------------------------------- out-of-line code
     for ln in e.stubs:
@@ -662,7 +765,7 @@ def render() -> str:
     lit = "\n".join('  "' + ln.replace('"', '\\"') + '\\n"' for ln in body.split("\n"))
     n = sum(1 for ln in body.split("\n") if ln and not ln.endswith(":"))
     clob = ", ".join([f'"v{i}"' for i in VGPR_CLOBBER] + [f'"a{i}"' for i in AGPR_CLOBBER] +
-                     ['"vcc"', '"m0"', '"scc"', '"memory"'])
+                     [f'"s{i}"' for i in SGPR_CLOBBER] + ['"vcc"', '"m0"', '"scc"', '"memory"'])
     return (HEADER + f"// {n} instructions.\n#define AAC_PW_ITEM_ASM \\\n" + " \\\n".join(lit.split("\n")) +
             "\n\n#define AAC_PW_CLOBBERS " + clob + "\n")
 

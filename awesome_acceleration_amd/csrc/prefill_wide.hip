@@ -62,7 +62,6 @@ namespace pw {
 using pf::Args;
 using pf::BKV;
 using pf::D;
-using pf::OPITCH;
 using pf::kRescale;
 
 constexpr int kWaves = 4;  // one per SIMD
@@ -71,6 +70,8 @@ constexpr int kRing = 4;                   // LDS stages
 constexpr int kTileBytes = BKV * D * 2;    // 16 KiB: one K or V tile
 constexpr int kStageBytes = 2 * kTileBytes;
 constexpr int kLdsBytes = kRing * kStageBytes;  // 128 KiB
+constexpr int kOutPitch = 136;             // output staging row pitch (bytes): 128 + 8
+constexpr int kOutBytes = 32 * kOutPitch;  // one wave's staging rows (half a column)
 constexpr int kLoadsPerTile = 8;           // direct loads per thread per tile (4 K + 4 V)
 
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
@@ -99,10 +100,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
   constexpr int BQ = 32 * WQ;
   static_assert(!F16, "the item body is written for bf16");
 
-  // LDS: kRing stages of [K tile | V tile]; after each item the ring stages
-  // the output tile (eight 32-row blocks of padded 256-byte rows).
-  static_assert(kWaves * 2 * 32 * OPITCH * 2 <= kLdsBytes, "output staging fits in the ring");
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[kLdsBytes];
+  // LDS: kRing stages of [K tile | V tile], filled in stream order: the
+  // tiles of consecutive items of this workgroup follow each other around the
+  // ring (item tile T at stage (g0 + T) % kRing).
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[kLdsBytes + kWaves * kOutBytes];
   const u32 lds0 = (u32)(uintptr_t)(lds_u8*)lds;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -184,12 +185,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     it.qb = CAUSAL ? nqb - 1 - z : z;
     return z < nqb;
   };
+  // segment bounds through scalar loads (the arrays are read-only here), so
+  // no vector-memory wait between items covers the body's loads in flight
+  typedef const int32_t __attribute__((address_space(4))) cint;
+  const cint* cuq = (const cint*)(uintptr_t)a.cu_q;
+  const cint* cuk = (const cint*)(uintptr_t)a.cu_k;
   auto next_item = [&](int& k, Item& it) -> bool {
     for (; k * P < n_items; ++k) {
       const int i = item_index(k);
       if (i >= n_items) continue;
       const int sg = seg_of(i);
-      if (decode(i, a.cu_q[sg], a.cu_q[sg + 1], a.cu_k[sg], a.cu_k[sg + 1], it)) return true;
+      if (decode(i, cuq[sg], cuq[sg + 1], cuk[sg], cuk[sg + 1], it)) return true;
     }
     return false;
   };
@@ -199,16 +205,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
                                              0x00020000);
   };
 
-  // Q fragments of both columns (B operand of S^T = K Q^T; lane = query).
-  // The 16 loads are issued from inline assembly: the compiler then does not
-  // track them and does not wait for them (and so for every tile load issued
-  // after them) ahead of the item body.  They are older than the item's tile
-  // loads, so the wait for tile 0 before the item's first barrier covers them.
+  // Q fragments of both columns (B operand of S^T = K Q^T; lane = query):
+  // this lane's address; the item body loads the next item's Q into qf at its
+  // end, the first item's come from load_q.  The loads are issued from inline
+  // assembly: the compiler does not track them and inserts no wait for them.
   u32x4 qf[2][8];
-  auto load_q = [&](const Item& it) {
+  auto q_addr = [&](const Item& it) {
     const int qi = it.qb * BQ + wq * 32 + col;
     const int qrow = it.q_beg + min(qi, max(it.Lq - 1, 0));
-    const u16* qp = a.q + (int64_t)qrow * a.q_stride + (it.h * G + 2 * wp) * D + hl * 8;
+    return a.q + (int64_t)qrow * a.q_stride + (it.h * G + 2 * wp) * D + hl * 8;
+  };
+  auto load_q = [&](const Item& it) {
+    const u16* qp = q_addr(it);
     asm volatile(
         "global_load_dwordx4 %0, %16, off\n\tglobal_load_dwordx4 %1, %16, off offset:32\n\t"
         "global_load_dwordx4 %2, %16, off offset:64\n\tglobal_load_dwordx4 %3, %16, off offset:96\n\t"
@@ -283,67 +291,55 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     return;
   }
   int kv_end = kv_end_of(cur);
-  __amdgpu_buffer_rsrc_t rsk, rsv;
-  auto set_rsrc = [&](const Item& it) {
-    rsk = rsrc_of(a.k + (int64_t)it.k_beg * a.k_stride + it.h * D, k_row_bytes, kv_end);
-    rsv = rsrc_of(a.v + (int64_t)it.k_beg * a.v_stride + it.h * D, v_row_bytes, kv_end);
-  };
-  set_rsrc(cur);
-
-  // tile T of the current item into stage T % kRing (past the last tile the
-  // resource range check reads zeros)
-  auto issue_tile = [&](int T) {
-    const u32 st = lds0 + (u32)((T % kRing) * kStageBytes) + (u32)(wave * 1024);
-    const int sk = T * BKV * k_row_bytes, sv = T * BKV * v_row_bytes;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      load_lds16(rsk, ld_voff_k, sk + i * 16 * k_row_bytes, st + i * 4096);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      load_lds16(rsv, ld_voff_v, sv + i * 16 * v_row_bytes, st + kTileBytes + i * 4096);
-  };
-  // the loads of all but the newest `n` tiles of this thread have landed
-  auto wait_tiles = [&](int n) {
-    if (n == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (n == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  };
-  // barrier without the compiler's full fence (which would also wait for
-  // every load in flight); LDS accesses are not moved across it
-  auto barrier = [&]() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  };
 
   const float cs = a.scale_log2;
   const float ncs = -cs;
   const float kthr = kRescale / cs;
   // per-lane constants of the item body: 4 hl (key offset of the lane half),
   // bpermute addresses of lanes (lane & 15) and (lane & 15) + 16, the lane's
-  // bit 4, and the byte address of this lane's first output element in the
-  // LDS staging area (wave's two 32-row blocks, row col, dims 4 hl ..)
+  // bit 4, and the byte offset of this lane's output (row col, dims 4 hl ..)
   const int hl4 = 4 * hl;
   const int bpa = (lane & 15) * 4, bpahi = ((lane & 15) + 16) * 4, hi16 = lane & 16;
-  const int obase = (int)lds0 + ((wave * 2) * 32 * OPITCH + col * OPITCH + 4 * hl) * 2;
+  // output: staging write / read addresses of this lane (wave's rows beside
+  // the ring), the global byte offset of its read-back row (8 rows of 128
+  // bytes per store) and the offset of eight rows
+  const int ostep = (int)(a.o_stride * 2);
+  const u32 stg = lds0 + (u32)(kLdsBytes + wave * kOutBytes);
+  const int stw = (int)stg + col * kOutPitch + 8 * hl;
+  const int str = (int)stg + (lane >> 3) * kOutPitch + 16 * (lane & 7);
+  const int osv = (lane >> 3) * ostep + 16 * (lane & 7);
+  const int ost8 = 8 * ostep;
   const u32 ldsw = lds0 + (u32)(wave * 1024);
   const int ks16 = 16 * k_row_bytes, vs16 = 16 * v_row_bytes;
   const int ks64 = 64 * k_row_bytes, vs64 = 64 * v_row_bytes;
 
-  // First item: Q and tiles 0-2 in flight.
-  load_q(cur);
-  issue_tile(0);
-  issue_tile(1);
-  issue_tile(2);
+  // First item: Q and tiles 0-2 (stream positions 0-2, stages 0-2; past its
+  // last tile the resource range check reads zeros).  Every later item finds
+  // its Q and first tiles loaded by the body of the item before it.
+  {
+    const __amdgpu_buffer_rsrc_t rsk =
+        rsrc_of(a.k + (int64_t)cur.k_beg * a.k_stride + cur.h * D, k_row_bytes, kv_end);
+    const __amdgpu_buffer_rsrc_t rsv =
+        rsrc_of(a.v + (int64_t)cur.k_beg * a.v_stride + cur.h * D, v_row_bytes, kv_end);
+    load_q(cur);
+    for (int T = 0; T < 3; ++T) {
+      const u32 st = lds0 + (u32)(T * kStageBytes) + (u32)(wave * 1024);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        load_lds16(rsk, ld_voff_k, T * ks64 + i * ks16, st + i * 4096);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        load_lds16(rsv, ld_voff_v, T * vs64 + i * vs16, st + kTileBytes + i * 4096);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  int g0 = 0;  // ring stage of the current item's tile 0
 
   for (;;) {
-    // segment bounds of the next round's item, loaded now (lane 0: start,
-    // lane 1: end) so they have arrived when this item ends
-    const int kc = k + 1, ic = item_index(kc);
-    const bool cand = kc * P < n_items && ic < n_items;
-    const int c_sg = (cand ? seg_of(ic) : 0) + (lane & 1);
-    const int c_q = a.cu_q[c_sg];
-    const int c_k = a.cu_k[c_sg];
+    Item nxt;
+    int kn = k + 1;
+    const bool more = next_item(kn, nxt);
+    const int kv_end_n = more ? kv_end_of(nxt) : 0;
 
     const int qi = cur.qb * BQ + wq * 32 + col;
     const int shift = cur.Lk - cur.Lq;
@@ -355,12 +351,24 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     const int my_lim = CAUSAL ? min(cur.Lk, qi + 1 + shift) : cur.Lk;
     const int nt = (kv_end + BKV - 1) / BKV;  // LDS tiles (workgroup-uniform)
     const int nsub = (w_end + 31) / 32;       // 32-key sub-tiles of this wave
+    // buffer ranges: this item's and the next item's K/V rows, this wave's
+    // output rows (none past the segment)
+    auto range = [&](int n, int row_bytes) {
+      return __builtin_amdgcn_readfirstlane(n > 0 ? (n - 1) * row_bytes + D * 2 : 0);
+    };
+    const u16* kb = a.k + (int64_t)cur.k_beg * a.k_stride + cur.h * D;
+    const u16* vb = a.v + (int64_t)cur.k_beg * a.v_stride + cur.h * D;
+    const u16* knb = more ? a.k + (int64_t)nxt.k_beg * a.k_stride + nxt.h * D : a.k;
+    const u16* vnb = more ? a.v + (int64_t)nxt.k_beg * a.v_stride + nxt.h * D : a.v;
+    const int kr = range(kv_end, k_row_bytes), vr = range(kv_end, v_row_bytes);
+    const int knr = range(kv_end_n, k_row_bytes), vnr = range(kv_end_n, v_row_bytes);
+    const int row0 = cur.qb * BQ + wq * 32;
+    const int orng = __builtin_amdgcn_readfirstlane(max(0, min(32, cur.Lq - row0)) * ostep);
+    const u16* ob = a.out + (int64_t)(cur.q_beg + row0) * a.o_stride + (cur.h * G + 2 * wp) * D;
+    const u16* qn = q_addr(more ? nxt : cur);  // the last item reloads its own Q (unused)
 
-    // tile 0 has landed for every wave (tiles 1, 2 may be in flight)
-    wait_tiles(2);
-    barrier();
-    // The item: O = softmax(Q K^T) V for both columns, normalised and
-    // written to this wave's LDS staging rows (see gen_prefill_wide_asm.py).
+    // The item: O = softmax(Q K^T) V for both columns, normalised and stored;
+    // the next item's Q and first tiles loaded (see gen_prefill_wide_asm.py).
     {
       int r_t, r_j, r0, r1, r2, r3, r5, r6, r_dm, r_dk, r_dv;
       unsigned long long r_ret;
@@ -369,68 +377,35 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
       asm volatile(AAC_PW_ITEM_ASM
                    : [t] "=&s"(r_t), [j] "=&s"(r_j), [s0] "=&s"(r0), [s1] "=&s"(r1), [s2] "=&s"(r2),
                      [s3] "=&s"(r3), [s5] "=&s"(r5), [s6] "=&s"(r6), [dm] "=&s"(r_dm), [dk] "=&s"(r_dk),
-                     [dv] "=&s"(r_dv), [ret] "=&s"(r_ret)
-                   : [q00] "v"(qf[0][0]), [q01] "v"(qf[0][1]), [q02] "v"(qf[0][2]), [q03] "v"(qf[0][3]),
-                     [q04] "v"(qf[0][4]), [q05] "v"(qf[0][5]), [q06] "v"(qf[0][6]), [q07] "v"(qf[0][7]),
-                     [q10] "v"(qf[1][0]), [q11] "v"(qf[1][1]), [q12] "v"(qf[1][2]), [q13] "v"(qf[1][3]),
-                     [q14] "v"(qf[1][4]), [q15] "v"(qf[1][5]), [q16] "v"(qf[1][6]), [q17] "v"(qf[1][7]),
-                     [ko0] "v"(koff[0]), [ko1] "v"(koff[1]), [ko2] "v"(koff[2]), [ko3] "v"(koff[3]),
+                     [dv] "=&s"(r_dv), [ret] "=&s"(r_ret),
+                     [q00] "+v"(qf[0][0]), [q01] "+v"(qf[0][1]), [q02] "+v"(qf[0][2]), [q03] "+v"(qf[0][3]),
+                     [q04] "+v"(qf[0][4]), [q05] "+v"(qf[0][5]), [q06] "+v"(qf[0][6]), [q07] "+v"(qf[0][7]),
+                     [q10] "+v"(qf[1][0]), [q11] "+v"(qf[1][1]), [q12] "+v"(qf[1][2]), [q13] "+v"(qf[1][3]),
+                     [q14] "+v"(qf[1][4]), [q15] "+v"(qf[1][5]), [q16] "+v"(qf[1][6]), [q17] "+v"(qf[1][7])
+                   : [ko0] "v"(koff[0]), [ko1] "v"(koff[1]), [ko2] "v"(koff[2]), [ko3] "v"(koff[3]),
                      [ko4] "v"(koff[4]), [ko5] "v"(koff[5]), [ko6] "v"(koff[6]), [ko7] "v"(koff[7]),
                      [vo0] "v"(voff[0]), [vo1] "v"(voff[1]), [vo2] "v"(voff[2]), [vo3] "v"(voff[3]),
                      [sel] "v"(sel), [cs] "s"(cs), [ncs] "s"(ncs), [kthr] "s"(kthr), [mylim] "v"(my_lim),
                      [hl4] "v"(hl4), [bpa] "v"(bpa), [bpahi] "v"(bpahi), [hi16] "v"(hi16),
-                     [obase] "v"(obase), [lds0] "s"(lds0), [ldsw] "s"(ldsw), [rsk] "s"(rsk), [rsv] "s"(rsv),
-                     [ldk] "v"(ld_voff_k), [ldv] "v"(ld_voff_v), [ks16] "s"(ks16), [vs16] "s"(vs16),
-                     [ks64] "s"(ks64), [vs64] "s"(vs64), [nsub] "s"(nsub), [wfull] "s"(w_full), [nt] "s"(nt)
+                     [lds0] "s"(lds0), [ldsw] "s"(ldsw), [ldk] "v"(ld_voff_k), [ldv] "v"(ld_voff_v),
+                     [ks16] "s"(ks16), [vs16] "s"(vs16), [ks64] "s"(ks64), [vs64] "s"(vs64),
+                     [nsub] "s"(nsub), [wfull] "s"(w_full), [nt] "s"(nt), [g0] "s"(g0),
+                     [kb] "s"(kb), [kr] "s"(kr), [vb] "s"(vb), [vr] "s"(vr),
+                     [knb] "s"(knb), [knr] "s"(knr), [vnb] "s"(vnb), [vnr] "s"(vnr),
+                     [ob] "s"(ob), [orng] "s"(orng), [stw] "v"(stw), [str] "v"(str), [osv] "v"(osv),
+                     [ost8] "s"(ost8), [qn] "v"(qn)
                    : AAC_PW_CLOBBERS);
 #pragma clang diagnostic pop
     }
-
-    // The next item (its Q loads go out once this item's are dead).
-    Item nxt;
-    int kn = kc;
-    bool more;
-    if (cand && decode(ic, __builtin_amdgcn_readlane(c_q, 0), __builtin_amdgcn_readlane(c_q, 1),
-                       __builtin_amdgcn_readlane(c_k, 0), __builtin_amdgcn_readlane(c_k, 1), nxt)) {
-      more = true;
-    } else {
-      kn = kc + 1;
-      more = kc * P < n_items && next_item(kn, nxt);
-    }
-    if (more) load_q(nxt);
-    // ---- store: each store instruction writes four whole 256-byte head rows
-    const u16* const ldsw16 = reinterpret_cast<const u16*>(lds);
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const u16* ob = ldsw16 + (wave * 2 + c) * (32 * OPITCH);
-      constexpr int kNt = 2;  // non-temporal stores
-      const int row0 = cur.qb * BQ + wq * 32;
-      const int nrow = min(32, cur.Lq - row0);
-      u16* og = a.out + (int64_t)(cur.q_beg + row0) * a.o_stride + (cur.h * G + 2 * wp + c) * D;
-      const int ostep = (int)(a.o_stride * 2);
-      const __amdgpu_buffer_rsrc_t ors =
-          __builtin_amdgcn_make_buffer_rsrc(og, 0, nrow > 0 ? nrow * ostep : 0, 0x00020000);
-      u32x4 val[8];
-#pragma unroll
-      for (int it = 0; it < 8; ++it)
-        val[it] = *reinterpret_cast<const u32x4*>(ob + (4 * it + (lane >> 4)) * OPITCH + (lane & 15) * 8);
-      const int voff_o = (lane >> 4) * ostep + (lane & 15) * 16;
-#pragma unroll
-      for (int it = 0; it < 8; ++it)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val[it]), ors, voff_o,
-                                               4 * it * ostep, kNt);
-    }
     if constexpr (STORE) own_store(cur);
     if (!more) break;
-    __syncthreads();  // output rows read back before the next item's tiles land
+    g0 = (g0 + nt) & 3;
     cur = nxt;
     k = kn;
-    kv_end = kv_end_of(cur);
-    set_rsrc(cur);
-    issue_tile(0);
-    issue_tile(1);
-    issue_tile(2);
+    kv_end = kv_end_n;
   }
+  // no load may still be writing LDS or registers when the workgroup ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   store_edges();
 }
 
