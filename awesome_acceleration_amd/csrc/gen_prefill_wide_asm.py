@@ -97,6 +97,8 @@ O_A, VF_A = 0, 160
 RK, RV, RKN, RVN = "s[88:91]", "s[92:95]", "s[80:83]", "s[84:87]"
 SGPR_CLOBBER = range(80, 96)
 KF_SET = [128, 224]
+N_OUT_STORES = 16   # output stores the body issues after the next item's Q loads
+N_OWN_STORES = 16   # and KV-cache stores (when it stores)
 VGPR_CLOBBER = range(152, 250)
 AGPR_CLOBBER = range(0, 256)
 
@@ -501,10 +503,17 @@ def build_rsrc(e, fixed_lo, base, rng):
 def generate() -> str:
     e = Emitter()
     # ---------------------------------------------------------------- entry
-    # This item's Q and first tiles were loaded before the previous item's 32
-    # output stores (the youngest memory operations): once at most 32 are in
-    # flight they have landed; the barrier makes that true for every wave.
-    e("s_waitcnt vmcnt(32)")
+    # This item's Q and first tiles were loaded before the previous item's
+    # output (and KV-cache) stores, the youngest memory operations of its
+    # body: once no more than those are in flight they have landed; the
+    # barrier makes that true for every wave.
+    e("s_cmp_eq_u32 %[dostore], 0")
+    e("s_cbranch_scc1 Lwait_out_%=")
+    e(f"s_waitcnt vmcnt({N_OUT_STORES + N_OWN_STORES})")
+    e("s_branch Lwaited_%=")
+    e("Lwait_out_%=:")
+    e(f"s_waitcnt vmcnt({N_OUT_STORES})")
+    e("Lwaited_%=:")
     e("s_waitcnt lgkmcnt(0)")
     build_rsrc(e, 88, "%[kb]", "%[kr]")
     build_rsrc(e, 92, "%[vb]", "%[vr]")
@@ -691,55 +700,113 @@ def generate() -> str:
     e("s_cmp_lt_u32 %[s2], 3")
     e("s_cbranch_scc1 Lmiss_%=")
     e("Lnomiss_%=:")
-    # (2) Q of the next item into the Q operands (their last reader, the
+    # (2) KV-cache store (when %[dostore]): this wave's own rows of the item
+    # (rows %[lrow] + 4 i of its share, 16 bytes at chunk l % 16) and their
+    # slots, loaded now from L2 (the tiles staged them moments ago) into the
+    # fragment AGPRs, dead after the loop; stored after the output.
+    e("s_cmp_eq_u32 %[dostore], 0")
+    e("s_cbranch_scc1 Lnoload_%=")
+    build_rsrc(e, 80, "%[okb]", "%[okr]")   # from the wave's first own row (not clamped to max_seqlen_k)
+    build_rsrc(e, 84, "%[ovb]", "%[ovr]")
+    build_rsrc(e, 88, "%[sb]", "%[srng]")
+    e("s_lshr_b32 %[s5], %[ks16], 2")     # 4 K rows
+    e("s_lshr_b32 %[s6], %[vs16], 2")     # 4 V rows
+    e("s_mov_b32 %[s2], 0")
+    e("s_mov_b32 %[s3], 0")
+    for i in range(8):
+        e(f"buffer_load_dwordx4 {ar(KF_SET[0] + 4 * i, 4)}, %[rvk], s[80:83], %[s2] offen")
+        e(f"buffer_load_dwordx4 {ar(VF_A + 4 * i, 4)}, %[rvv], s[84:87], %[s3] offen")
+        e(f"buffer_load_dwordx2 {ar(VF_A + 32 + 2 * i, 2)}, %[slv], s[88:91], 0 offen offset:{32 * i}")
+        if i < 7:
+            e("s_add_u32 %[s2], %[s2], %[s5]")
+            e("s_add_u32 %[s3], %[s3], %[s6]")
+    e("Lnoload_%=:")
+    # (3) Q of the next item into the Q operands (their last reader, the
     # score MFMAs, issued long ago)
     for c in range(2):
         for t in range(8):
             e(f"global_load_dwordx4 %[q{c}{t}], %[qn], off offset:{256 * c + 32 * t}")
-    # (3) O / l rounded to bf16, through this wave's LDS staging rows (beside
+    # (4) O / l rounded to bf16, through this wave's LDS staging rows (beside
     # the ring: 32 rows x 128 bytes at a 136-byte pitch, one half of a column
     # at a time) to whole 128-byte row segments in global memory.  Lane l
     # holds query l % 32, dims 32 db + 8 i + 4 (l / 32) + 0..3 of register
-    # group i; rows past the segment fall outside the output resource.
+    # group i; rows past the segment fall outside the output resource.  A
+    # wave's LDS operations execute in order, so a half's reads follow its
+    # writes and the next half's writes follow those reads with no wait; only
+    # the global stores wait for the read data.  The address registers (dead
+    # after the loop) take 16 accumulators at a time, the score registers the
+    # read-back rows.
     build_rsrc(e, 88, "%[ob]", "%[orng]")
     e("s_nop 7")
     e("s_nop 7")
     e("s_nop 7")
-    n_pair = 0
+    e(f"ds_bpermute_b32 {v(T0)}, %[bpa], {v(L[0])}")
+    e(f"ds_bpermute_b32 {v(T1)}, %[bpa], {v(L[0] + 1)}")
+    e(f"ds_bpermute_b32 {v(T2)}, %[bpa], {v(L[1])}")
+    e(f"ds_bpermute_b32 {v(T3)}, %[bpa], {v(L[1] + 1)}")
+    e("s_waitcnt lgkmcnt(0)")
+    e(f"v_cmp_ne_u32 vcc, 0, %[hi16]")
+    e(f"v_cndmask_b32 {v(T0)}, {v(T0)}, {v(T1)}, vcc")        # row sum of this lane's query, column 0
+    e(f"v_cndmask_b32 {v(T2)}, {v(T2)}, {v(T3)}, vcc")        # column 1
+    e(f"v_rcp_f32 {v(T1)}, {v(T0)}")
+    e(f"v_rcp_f32 {v(T3)}, {v(T2)}")
+    e(f"v_cmp_lt_f32 vcc, 0, {v(T0)}")
+    e(f"v_cndmask_b32 {v(T1)}, 0, {v(T1)}, vcc")              # 1/l, 0 for an empty row
+    e(f"v_cmp_lt_f32 vcc, 0, {v(T2)}")
+    e(f"v_cndmask_b32 {v(T3)}, 0, {v(T3)}, vcc")
+    n_out = 0
     for x in range(2):
-        e(f"ds_bpermute_b32 {v(T0)}, %[bpa], {v(L[x])}")
-        e(f"ds_bpermute_b32 {v(T1)}, %[bpa], {v(L[x] + 1)}")
-        e("s_waitcnt lgkmcnt(0)")
-        e(f"v_cmp_ne_u32 vcc, 0, %[hi16]")
-        e(f"v_cndmask_b32 {v(T0)}, {v(T0)}, {v(T1)}, vcc")        # row sum of this lane's query
-        e(f"v_rcp_f32 {v(T1)}, {v(T0)}")
-        e(f"v_cmp_lt_f32 vcc, 0, {v(T0)}")
-        e(f"v_cndmask_b32 {v(T1)}, 0, {v(T1)}, vcc")              # 1/l, 0 for an empty row
-        e("s_nop 1")
+        inv = v(T1) if x == 0 else v(T3)
         base = O_A + 64 * x
         for hh in range(2):
             for db in (2 * hh, 2 * hh + 1):
+                for i in range(16):
+                    e(f"v_accvgpr_read_b32 {v(KA + i)}, a{base + 16 * db + i}")
+                for i in range(16):
+                    e(f"v_mul_f32 {v(KA + i)}, {v(KA + i)}, {inv}")
+                pb = P[db % 2]
                 for r in range(4):
-                    a0 = base + 16 * db + 4 * r
-                    for i in range(4):
-                        e(f"v_accvgpr_read_b32 {v(SCR + i)}, a{a0 + i}")
-                    for i in range(4):
-                        e(f"v_mul_f32 {v(SCR + i)}, {v(SCR + i)}, {v(T1)}")
-                    out = SCR + 4 + 2 * (n_pair % 2)   # alternate pairs between writes
-                    n_pair += 1
-                    e(f"v_cvt_pk_bf16_f32 {v(out)}, {v(SCR)}, {v(SCR + 1)}")
-                    e(f"v_cvt_pk_bf16_f32 {v(out + 1)}, {v(SCR + 2)}, {v(SCR + 3)}")
-                    e(f"ds_write_b64 %[stw], {vr(out, 2)} offset:{64 * (db % 2) + 16 * r}")
-            e("s_waitcnt lgkmcnt(0)")
-            # rows 8 i + l / 8, bytes 16 (l % 8) of the half (the scores' registers are free)
+                    e(f"v_cvt_pk_bf16_f32 {v(pb + 2 * r)}, {v(KA + 4 * r)}, {v(KA + 4 * r + 1)}")
+                    e(f"v_cvt_pk_bf16_f32 {v(pb + 2 * r + 1)}, {v(KA + 4 * r + 2)}, {v(KA + 4 * r + 3)}")
+                for r in range(4):
+                    e(f"ds_write_b64 %[stw], {vr(pb + 2 * r, 2)} offset:{64 * (db % 2) + 16 * r}")
+            # rows 8 i + l / 8, bytes 16 (l % 8) of the half
             for i in range(4):
-                e(f"ds_read_b128 {vr(S[0] + 4 * i, 4)}, %[str] offset:{1088 * i}")
-            e("s_waitcnt lgkmcnt(0)")
+                e(f"ds_read_b128 {vr(S[hh] + 4 * i, 4)}, %[str] offset:{1088 * i}")
+        e("s_waitcnt lgkmcnt(0)")
+        for hh in range(2):
             e("s_mov_b32 %[s2], 0")
             for i in range(4):
-                e(f"buffer_store_dwordx4 {vr(S[0] + 4 * i, 4)}, %[osv], {RK}, %[s2] offen offset:{256 * x + 128 * hh}")
+                e(f"buffer_store_dwordx4 {vr(S[hh] + 4 * i, 4)}, %[osv], {RK}, %[s2] offen offset:{256 * x + 128 * hh}")
+                n_out += 1
                 if i < 3:
                     e("s_add_u32 %[s2], %[s2], %[ost8]")
+    assert n_out == N_OUT_STORES, n_out
+    # (5) the own rows into the KV caches: row valid when within the wave's
+    # share and its slot in [0, num_rows); an invalid row's offset falls
+    # outside the cache resource.  The rows' loads are older than the 16 Q
+    # loads and the output stores.
+    e("s_cmp_eq_u32 %[dostore], 0")
+    e("s_cbranch_scc1 Lnostore_%=")
+    e(f"s_waitcnt vmcnt({16 + N_OUT_STORES})")
+    build_rsrc(e, 88, "%[kcb]", "%[crng]")
+    build_rsrc(e, 92, "%[vcb]", "%[crng]")
+    e("s_mov_b32 s80, %[nrows]")
+    e("s_mov_b32 s81, 0")
+    for i in range(8):
+        e(f"v_accvgpr_read_b32 {v(T0)}, a{VF_A + 32 + 2 * i}")
+        e(f"v_accvgpr_read_b32 {v(T1)}, a{VF_A + 33 + 2 * i}")
+        e(f"s_sub_u32 %[s2], %[nvalid], {4 * i}")
+        e(f"v_cmp_gt_i32 %[ret], %[s2], %[lrow]")                # row within the share
+        e(f"v_cmp_gt_u64 vcc, s[80:81], {vr(T0, 2)}")            # slot in [0, num_rows)
+        e("s_and_b64 vcc, vcc, %[ret]")
+        e(f"v_mul_lo_u32 {v(T2)}, {v(T0)}, %[cstride]")
+        e(f"v_add_u32 {v(T2)}, {v(T2)}, %[chunk16]")
+        e(f"v_cndmask_b32 {v(T2)}, -1, {v(T2)}, vcc")
+        e(f"buffer_store_dwordx4 {ar(KF_SET[0] + 4 * i, 4)}, {v(T2)}, s[88:91], 0 offen")
+        e(f"buffer_store_dwordx4 {ar(VF_A + 4 * i, 4)}, {v(T2)}, s[92:95], 0 offen")
+    assert 2 * 8 == N_OWN_STORES
+    e("Lnostore_%=:")
     e("s_branch Lend_%=")
     # ------------------------------------------------- out-of-line code
     for ln in e.stubs:

@@ -810,7 +810,9 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
                        : pf::launch_g<true, false, false, true>(a, g, max_seqlen_q, n_cu, stream))
                 : (f16 ? pf::launch_g<false, true, false, true>(a, g, max_seqlen_q, n_cu, stream)
                        : pf::launch_g<false, false, false, true>(a, g, max_seqlen_q, n_cu, stream));
-  } else if (prefill_wide_supports(g, scale, f16))
+  } else if (prefill_wide_supports(g, scale, f16) &&
+             (n_store == 0 || num_cache_rows * n_kv_heads * head_dim * 2 < (int64_t(1) << 32)))
+    // the wide kernel's cache store addresses a head's rows with 32-bit offsets
     rc = prefill_wide_launch(a, g, causal != 0, n_store > 0, max_seqlen_q, n_cu, stream);
   else if (n_store > 0)  // the store variant exists for causal attention only
     rc = f16 ? pf::launch_g<true, true, true>(a, g, max_seqlen_q, n_cu, stream)

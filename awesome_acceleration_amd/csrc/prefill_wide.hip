@@ -236,44 +236,22 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
 
   // ---- the KV-cache store (STORE).  Each item stores the K/V rows of its own
   // q-block (its queries' rows taken as keys, since cu_q == cu_k) for its KV
-  // head after its output (the tiles staged those rows moments before, so
-  // they come from L2), in batches of four 16-row passes.  The item of rank 0
-  // of a segment also stores the q-blocks no item owns (a max_seqlen_q below
-  // the segment's length), and workgroup 0 the tokens before cu[0] and from
-  // cu[n] on.  Every token's rows are thus written at least once; a row
-  // written twice gets the same bytes both times.
-  constexpr int NP = BQ / 16;  // passes of 16 rows (16 threads per row)
-  constexpr int NB = NP < 4 ? NP : 4;
-  auto own_store = [&](const Item& it) {
-    pf::KArgs* sa = pf::kernel_args();
-    const int r0 = it.qb * BQ;
-    const int nr = min(BQ, it.Lq - r0);  // >= 1 for an existing item
-#pragma unroll
-    for (int p0 = 0; p0 < NP; p0 += NB) {
-      int64_t csl[NB];
-      u32x4 ck[NB], cv[NB];
-#pragma unroll
-      for (int i = 0; i < NB; ++i) {  // rows past the q-block repeat its last row
-        const int rr = min((tid >> 4) + 16 * (p0 + i), nr - 1);
-        const int64_t t = (int64_t)it.k_beg + r0 + rr;
-        const int64_t tok = min(t, (int64_t)sa->n_tok - 1);
-        csl[i] = t < sa->n_tok ? sa->slots[tok] : -1;
-        ck[i] = *reinterpret_cast<const u32x4*>(a.k + tok * a.k_stride + it.h * D + (tid & 15) * 8);
-        cv[i] = *reinterpret_cast<const u32x4*>(a.v + tok * a.v_stride + it.h * D + (tid & 15) * 8);
-      }
-#pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        if ((uint64_t)csl[i] < (uint64_t)sa->num_rows) {
-          const int64_t dst = (csl[i] * a.hkv + it.h) * D + (tid & 15) * 8;
-          *reinterpret_cast<u32x4*>(sa->kc + dst) = ck[i];
-          *reinterpret_cast<u32x4*>(sa->vc + dst) = cv[i];
-        }
-      }
-    }
+  // head: the item body loads them from L2 (the tiles staged them moments
+  // before) right after its tile loop and writes them to the caches after the
+  // output, each wave its share of 64 / G rows.  The item of rank 0 of a
+  // segment also stores the q-blocks no item owns (a max_seqlen_q below the
+  // segment's length), and workgroup 0 the tokens before cu[0] and from cu[n]
+  // on.  Every token's rows are thus written at least once; a row written
+  // twice gets the same bytes both times.
+  constexpr int kShare = 64 / G;               // own rows per wave
+  const int share0 = wq * 32 + wp * kShare;    // the wave's first own row in a q-block
+  auto store_unowned = [&](const Item& it) {
     const int nqb = (it.Lq + BQ - 1) / BQ;
     if (nqb - 1 - it.qb == 0 && nqb > a.n_qblocks) {  // rank 0 (causal numbering)
       const int lo = nqb - a.n_qblocks;               // q-blocks [lo, nqb) have items
       pf::store_kv_span<kThreads>(a, tid, it.k_beg, it.k_beg + (int64_t)lo * BQ, it.h, it.h + 1);
+      // the next item body's first wait counts only its predecessor's stores
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
   };
   // workgroup 0: tokens outside [cu[0], cu[n])
@@ -309,6 +287,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
   const int str = (int)stg + (lane >> 3) * kOutPitch + 16 * (lane & 7);
   const int osv = (lane >> 3) * ostep + 16 * (lane & 7);
   const int ost8 = 8 * ostep;
+  // KV-cache store: lane's row within a group of 4 and byte chunk within a
+  // row, slot offset of that row, cache head-row stride and the caches' byte
+  // range from the head's first row (the host keeps it below 4 GiB)
+  const int lrow = lane >> 4, chunk16 = 16 * (lane & 15), slv = 8 * lrow;
+  const int rvk = lrow * k_row_bytes + chunk16, rvv = lrow * v_row_bytes + chunk16;
+  int cstride = 0, crng = 0, nrows = 0;
+  if constexpr (STORE) {
+    pf::KArgs* sa = pf::kernel_args();
+    cstride = a.hkv * D * 2;
+    nrows = (int)sa->num_rows;
+    // from a head's base: rows 0..num_rows-1 (a slot past them is refused per row)
+    crng = sa->num_rows > 0 ? (int)((sa->num_rows - 1) * cstride + D * 2) : 0;
+  }
   const u32 ldsw = lds0 + (u32)(wave * 1024);
   const int ks16 = 16 * k_row_bytes, vs16 = 16 * v_row_bytes;
   const int ks64 = 64 * k_row_bytes, vs64 = 64 * v_row_bytes;
@@ -366,6 +357,25 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     const int orng = __builtin_amdgcn_readfirstlane(max(0, min(32, cur.Lq - row0)) * ostep);
     const u16* ob = a.out + (int64_t)(cur.q_beg + row0) * a.o_stride + (cur.h * G + 2 * wp) * D;
     const u16* qn = q_addr(more ? nxt : cur);  // the last item reloads its own Q (unused)
+    // KV-cache store of the wave's own rows (STORE; inert operands otherwise)
+    int nvalid = 0, srng = 0, okr = 0, ovr = 0;
+    const int64_t* sb = a.slots;
+    const u16 *kcb = a.k, *vcb = a.v, *okb = a.k, *ovb = a.v;
+    if constexpr (STORE) {
+      pf::KArgs* sa = pf::kernel_args();
+      const int r0 = cur.qb * BQ + share0;              // first own row (in the segment)
+      const int64_t t0 = (int64_t)cur.k_beg + r0;       // its token
+      const int64_t tok_left = max((int64_t)0, (int64_t)sa->n_tok - t0);
+      nvalid = __builtin_amdgcn_readfirstlane((int)min((int64_t)max(0, min(kShare, cur.Lq - r0)), tok_left));
+      srng = __builtin_amdgcn_readfirstlane((int)min(tok_left, (int64_t)32) * 8);
+      sb = sa->slots + t0;
+      kcb = sa->kc + cur.h * D;
+      vcb = sa->vc + cur.h * D;
+      okb = a.k + t0 * a.k_stride + cur.h * D;
+      ovb = a.v + t0 * a.v_stride + cur.h * D;
+      okr = range(nvalid, k_row_bytes);
+      ovr = range(nvalid, v_row_bytes);
+    }
 
     // The item: O = softmax(Q K^T) V for both columns, normalised and stored;
     // the next item's Q and first tiles loaded (see gen_prefill_wide_asm.py).
@@ -393,11 +403,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
                      [kb] "s"(kb), [kr] "s"(kr), [vb] "s"(vb), [vr] "s"(vr),
                      [knb] "s"(knb), [knr] "s"(knr), [vnb] "s"(vnb), [vnr] "s"(vnr),
                      [ob] "s"(ob), [orng] "s"(orng), [stw] "v"(stw), [str] "v"(str), [osv] "v"(osv),
-                     [ost8] "s"(ost8), [qn] "v"(qn)
+                     [ost8] "s"(ost8), [qn] "v"(qn), [dostore] "s"((int)STORE), [sb] "s"(sb), [okb] "s"(okb), [okr] "s"(okr), [ovb] "s"(ovb), [ovr] "s"(ovr),
+                     [srng] "s"(srng), [kcb] "s"(kcb), [vcb] "s"(vcb), [crng] "s"(crng),
+                     [cstride] "s"(cstride), [nrows] "s"(nrows), [nvalid] "s"(nvalid), [rvk] "v"(rvk),
+                     [rvv] "v"(rvv), [slv] "v"(slv), [lrow] "v"(lrow), [chunk16] "v"(chunk16)
                    : AAC_PW_CLOBBERS);
 #pragma clang diagnostic pop
     }
-    if constexpr (STORE) own_store(cur);
+    if constexpr (STORE) store_unowned(cur);
     if (!more) break;
     g0 = (g0 + nt) & 3;
     cur = nxt;
