@@ -380,9 +380,17 @@ def slot(e, c, par, extra=None):
         compare(e, c)
 
 
+def q_load(c, t):
+    """One fragment of the next item's Q (column c, 16-dim step t)."""
+    return f"global_load_dwordx4 %[q{c}{t}], %[qn], off offset:{256 * c + 32 * t}"
+
+
 def last(e, par):
     """Last sub-tile j of the wave (par = j % 2): softmax of S1(j) -> P1(j),
-    then O0 += V(j) P0(j) and O1 += V(j) P1(j)."""
+    then O0 += V(j) P0(j) and O1 += V(j) P1(j).  No score MFMA reads Q any
+    more, so the next item's Q loads go out here, one beside each MFMA (each
+    spans 32 query rows: issued in a burst they hold the wave for ~2000
+    cycles); %[qd] records that they did."""
     sm = softmax_ops(1)
     e("s_waitcnt lgkmcnt(0)")
     for i in range(8):
@@ -392,6 +400,7 @@ def last(e, par):
             check_branch(e, 1)
         for op in sm[i]:
             e(op)
+        e(q_load(0, i))
     for i in range(8, 18):
         e("s_nop 0")
         for op in sm[i]:
@@ -402,6 +411,8 @@ def last(e, par):
     for i in range(8):
         f, db, tt = pv_frag(8 + i)
         e(f"{MFMA} {O_t(1, db)}, {VF(par, f)}, {P_t(1, tt)}, {O_t(1, db)}")
+        e(q_load(1, i))
+    e("s_mov_b32 %[qd], 1")
 
 
 def rescale_sub(e, x):
@@ -519,6 +530,7 @@ def generate() -> str:
     build_rsrc(e, 92, "%[vb]", "%[vr]")
     build_rsrc(e, 80, "%[knb]", "%[knr]")
     build_rsrc(e, 84, "%[vnb]", "%[vnr]")
+    e("s_mov_b32 %[qd], 0")
     e("s_barrier")
     for i in range(4):
         e(f"v_mov_b32 {v(ZERO + i)}, 0")
@@ -721,11 +733,14 @@ def generate() -> str:
             e("s_add_u32 %[s2], %[s2], %[s5]")
             e("s_add_u32 %[s3], %[s3], %[s6]")
     e("Lnoload_%=:")
-    # (3) Q of the next item into the Q operands (their last reader, the
-    # score MFMAs, issued long ago)
+    # (3) Q of the next item into the Q operands, unless the wave's last
+    # sub-tile loaded it (a wave without queries has none)
+    e("s_cmp_eq_u32 %[qd], 0")
+    e("s_cbranch_scc0 Lqdone_%=")
     for c in range(2):
         for t in range(8):
-            e(f"global_load_dwordx4 %[q{c}{t}], %[qn], off offset:{256 * c + 32 * t}")
+            e(q_load(c, t))
+    e("Lqdone_%=:")
     # (4) O / l rounded to bf16, through this wave's LDS staging rows (beside
     # the ring: 32 rows x 128 bytes at a 136-byte pitch, one half of a column
     # at a time) to whole 128-byte row segments in global memory.  Lane l
@@ -784,11 +799,11 @@ def generate() -> str:
     assert n_out == N_OUT_STORES, n_out
     # (5) the own rows into the KV caches: row valid when within the wave's
     # share and its slot in [0, num_rows); an invalid row's offset falls
-    # outside the cache resource.  The rows' loads are older than the 16 Q
-    # loads and the output stores.
+    # outside the cache resource.  The rows' loads are older than the output
+    # stores (and younger than the Q loads, unless the epilogue issued those).
     e("s_cmp_eq_u32 %[dostore], 0")
     e("s_cbranch_scc1 Lnostore_%=")
-    e(f"s_waitcnt vmcnt({16 + N_OUT_STORES})")
+    e(f"s_waitcnt vmcnt({N_OUT_STORES})")
     build_rsrc(e, 88, "%[kcb]", "%[crng]")
     build_rsrc(e, 92, "%[vcb]", "%[crng]")
     e("s_mov_b32 s80, %[nrows]")

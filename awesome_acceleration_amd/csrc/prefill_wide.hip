@@ -380,14 +380,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     // The item: O = softmax(Q K^T) V for both columns, normalised and stored;
     // the next item's Q and first tiles loaded (see gen_prefill_wide_asm.py).
     {
-      int r_t, r_j, r0, r1, r2, r3, r5, r6, r_dm, r_dk, r_dv;
+      int r_t, r_j, r0, r1, r2, r3, r5, r6, r_dm, r_dk, r_dv, r_qd;
       unsigned long long r_ret;
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
       asm volatile(AAC_PW_ITEM_ASM
                    : [t] "=&s"(r_t), [j] "=&s"(r_j), [s0] "=&s"(r0), [s1] "=&s"(r1), [s2] "=&s"(r2),
                      [s3] "=&s"(r3), [s5] "=&s"(r5), [s6] "=&s"(r6), [dm] "=&s"(r_dm), [dk] "=&s"(r_dk),
-                     [dv] "=&s"(r_dv), [ret] "=&s"(r_ret),
+                     [dv] "=&s"(r_dv), [qd] "=&s"(r_qd), [ret] "=&s"(r_ret),
                      [q00] "+v"(qf[0][0]), [q01] "+v"(qf[0][1]), [q02] "+v"(qf[0][2]), [q03] "+v"(qf[0][3]),
                      [q04] "+v"(qf[0][4]), [q05] "+v"(qf[0][5]), [q06] "+v"(qf[0][6]), [q07] "+v"(qf[0][7]),
                      [q10] "+v"(qf[1][0]), [q11] "+v"(qf[1][1]), [q12] "+v"(qf[1][2]), [q13] "+v"(qf[1][3]),

@@ -37,6 +37,9 @@ Also reported on the same line:
                 (the same call unsplit beside it);
   prefill_long  the same kernel on 8 x 8192 causal tokens: its steady-state
                 rate, where per-item start and epilogue costs are small;
+  prefill_engine  the prefill call the engine makes for 256 fresh 1024-token
+                requests: 256 x 1024 causal tokens with the paged store,
+                about 64 work items per CU;
   decode_fp32_small  the fp32 decode of the CPU-runnable case (4 seqs,
                 contexts 17/64/200/511) on the GPU, with its host figure;
   e2e           random-init Qwen3-0.6B, 256 requests x 1024 input / 1024
@@ -78,6 +81,8 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_PROFILE = "profiles/decode_256seq_ctx1k-2k_bf16_traffic.md"
 TRAFFIC_PREFILL = "profiles/prefill_8x1024_bf16_traffic.md"
+TRAFFIC_PREFILL_LONG = "profiles/prefill_8x8192_bf16_traffic.md"
+TRAFFIC_PREFILL_ENGINE = "profiles/prefill_engine_256x1024_bf16_traffic.md"
 TRAFFIC_DECODE_LONG = "profiles/decode_long_64seq_ctx16k-32k_bf16_traffic.md"
 TRAFFIC_KV_EXPORT = "profiles/kv_export_2048tok_28layers_bf16_traffic.md"
 DEVICE_PROFILE = "profiles/device_mi355x.md"
@@ -114,6 +119,8 @@ def parse():
     p.add_argument("--no-long", action="store_true", help="skip the long-context GQA-4 decode leg")
     p.add_argument("--no-slot", action="store_true", help="skip the slot-layout decode leg")
     p.add_argument("--no-prefill-long", action="store_true", help="skip the 8 x 8192 prefill leg")
+    p.add_argument("--no-prefill-engine", action="store_true",
+                   help="skip the 256 x 1024 prefill leg (the engine's prefill call)")
     p.add_argument("--no-kv", action="store_true", help="skip the KV export/import leg")
     p.add_argument("--no-tp2", action="store_true", help="skip the TP=2 per-rank shape leg")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine leg")
@@ -122,7 +129,7 @@ def parse():
     p.add_argument("--e2e-out", type=int, default=1024)
     p.add_argument("--only", choices=["decode", "decode_fp32_small", "decode_slot", "decode_long",
                                       "tp2_rank", "kv_transfer",
-                                      "prefill", "prefill_one", "prefill_long", "e2e"],
+                                      "prefill", "prefill_one", "prefill_long", "prefill_engine", "e2e"],
                    default=None,
                    help="run one leg only (for profiling)")
     return p.parse_args()
@@ -468,7 +475,57 @@ def bench_prefill_long(torch, fai, dev, args, nseq=8, L=8192, hq=16, hkv=8):
         "us_attend": round(t * 1e6, 2),
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
-                     "flops_per_launch": flops, "traffic": None},
+                     "flops_per_launch": flops, "traffic": measured_traffic(TRAFFIC_PREFILL_LONG),
+                     "traffic_source": TRAFFIC_PREFILL_LONG},
+    }
+
+
+def bench_prefill_engine(torch, fai, paged, dev, args, nseq=256, L=1024, hq=16, hkv=8):
+    """The prefill call the continuous-batching engine makes for 256 fresh
+    1024-token requests (llm.py:116-184): one launch over 256 packed causal
+    segments with the store into a shuffled paged cache (block 256), about 64
+    work items per CU -- the per-item start and epilogue weigh here."""
+    d, bs, N = 128, 256, nseq * L
+    nb = -(-L // bs)
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    qkv = torch.randn((N, (hq + 2 * hkv) * d), generator=g, device=dev).to(torch.bfloat16)
+    q = qkv[:, :hq * d].view(N, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].contiguous().view(N, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(N, hkv, d)
+    rs = np.random.RandomState(args.seed)
+    perm = rs.permutation(nseq * nb).astype(np.int32)
+    cu, _, sm = paged.build_prefill_metadata([L] * nseq, perm.reshape(nseq, nb), bs, dev)
+    kc = torch.zeros((nseq * nb, bs, hkv, d), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    flops = 4 * hq * d * nseq * (L * (L + 1) // 2)
+
+    def step():
+        return fai.varlen_prefill_with_kvcache(q, k, v, cu, L, kc, vc, sm, causal=True)
+
+    def attend():
+        return fai.flash_attn_varlen_func(q, k, v, cu, cu, L, L, causal=True)
+
+    for _ in range(3):
+        step()
+        attend()
+    warm(torch, [step, attend], args.warmup_seconds)
+    n = max(5, args.steps // 5)
+    t_step = launch_avg(torch, step, n)
+    t = launch_avg(torch, attend, n)
+    ach, ach_s = flops / t / 1e12, flops / t_step / 1e12
+    return {
+        "workload": f"varlen causal prefill {nseq} x {L} tokens with the KV store into a paged cache "
+                    f"(block {bs}, shuffled), {hq}/{hkv} heads, head_dim 128, bf16",
+        "us_step_with_store": round(t_step * 1e6, 2),
+        "us_attend": round(t * 1e6, 2),
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+                     "frac_with_store": round(ach_s / BF16_PEAK_TFLOPS, 4),
+                     "flops_per_launch": flops,
+                     "traffic": measured_traffic(TRAFFIC_PREFILL_ENGINE),
+                     "traffic_with_store": measured_traffic(TRAFFIC_PREFILL_ENGINE,
+                                                            "traffic_bytes_per_launch_store"),
+                     "traffic_source": TRAFFIC_PREFILL_ENGINE},
     }
 
 
@@ -868,6 +925,9 @@ def main():
     if args.only in (None, "prefill_long") and not args.no_prefill_long:
         res["prefill_long"] = bench_prefill_long(torch, fai, dev, args)
         torch.cuda.empty_cache()
+    if args.only in (None, "prefill_engine") and not args.no_prefill_engine:
+        res["prefill_engine"] = bench_prefill_engine(torch, fai, paged, dev, args)
+        torch.cuda.empty_cache()
     if args.only in (None, "e2e") and not args.no_e2e:
         res["e2e"] = bench_e2e(torch, args)
     if args.only is not None:
@@ -940,6 +1000,8 @@ def main():
         line["decode_slot"] = res["decode_slot"]
     if "prefill_long" in res:
         line["prefill_long"] = res["prefill_long"]
+    if "prefill_engine" in res:
+        line["prefill_engine"] = res["prefill_engine"]
     if "prefill_one_request" in res:
         line["prefill_one_request"] = res["prefill_one_request"]
     if "tp2_rank" in res:
