@@ -28,6 +28,7 @@ struct Args {
   float scale_log2;
   u16* out;
   int32_t n_qblocks;  // q-blocks of the longest segment
+  int32_t chunk_segs; // segments per item chunk (wide kernel: items are numbered chunk by chunk)
   int32_t max_k;      // max_seqlen_k: bounds every segment's key count
   // KV-cache store in the same kernel (self-attention, cu_q == cu_k): token
   // t's K/V rows go to cache row slots[t] of the [num_rows, hkv, D] caches

@@ -150,13 +150,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     for (int i = 0; i < 4; ++i) sel[i] = one ? 0x3f803f80u : 0u;  // bf16 ones
   }
 
-  // ---- work items (q-block rank z, segment s, KV head h), rank-major so the
-  // heaviest causal q-blocks come first.  Persistent grid: workgroup w of P
-  // takes item k P + w in even rounds and, in odd rounds, the mirror image
-  // taken in groups of eight (item (k+1) P - 8 - 8 (w/8) + w%8 when P is a
-  // multiple of 8): heavy items pair with light ones, and item i mod 8 stays
-  // equal to w mod 8, so with eight KV heads each head's K/V rows are read
-  // by one XCD's workgroups (workgroups are dealt to the 8 XCDs round-robin).
+  // ---- work items (q-block rank z, segment s, KV head h), rank-major inside
+  // each chunk of segments (below) so a chunk's heaviest causal q-blocks come
+  // first.  Persistent grid: workgroup w of P takes item k P + w in even
+  // rounds and, in odd rounds, the mirror image taken in groups of eight
+  // (item (k+1) P - 8 - 8 (w/8) + w%8 when P is a multiple of 8): heavy items
+  // pair with light ones, and item i mod 8 stays equal to w mod 8, so with
+  // eight KV heads each head's K/V rows are read by one XCD's workgroups
+  // (workgroups are dealt to the 8 XCDs round-robin).
   struct Item {
     int h, s, qb, q_beg, Lq, k_beg, Lk;
   };
@@ -167,16 +168,34 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     if (!(k & 1)) return k * P + w;
     return (P & 7) == 0 ? (k + 1) * P - 8 - (w & ~7) + (w & 7) : (k + 1) * P - 1 - w;
   };
-  auto seg_of = [&](int i) { return (i % n_hs) / a.hkv; };
+  // Items are numbered chunk by chunk: a chunk is chunk_segs consecutive
+  // segments (the last may be shorter), numbered rank-major inside (rank z,
+  // segment, KV head).  A chunk's K/V rows per head are sized to about half
+  // an XCD's L2, so the workgroups of one XCD (one KV head with eight KV
+  // heads) stream a few segments at a time and re-read their tiles from L2.
+  const int per_chunk = a.chunk_segs * a.n_qblocks * a.hkv;  // items in a full chunk
+  struct Place {
+    int z, s, h;
+  };
+  auto place_of = [&](int i) {
+    const int c = i / per_chunk;
+    const int r = i - c * per_chunk;
+    const int cs = min(a.chunk_segs, a.n_seqs - c * a.chunk_segs);  // segments in chunk c
+    const int z = r / (cs * a.hkv);
+    const int rem = r - z * cs * a.hkv;
+    const int sl = rem / a.hkv;
+    return Place{z, c * a.chunk_segs + sl, rem - sl * a.hkv};
+  };
+  auto seg_of = [&](int i) { return place_of(i).s; };
   auto kv_end_of = [&](const Item& it) {
     const int wg_qmax = min(it.qb * BQ + BQ, it.Lq) - 1;
     return CAUSAL ? max(0, min(it.Lk, wg_qmax + 1 + it.Lk - it.Lq)) : it.Lk;
   };
   auto decode = [&](int i, int q0, int q1, int k0, int k1, Item& it) -> bool {
-    const int z = i / n_hs;
-    const int hs = i - z * n_hs;
-    it.s = hs / a.hkv;
-    it.h = hs - it.s * a.hkv;
+    const Place pl = place_of(i);
+    const int z = pl.z;
+    it.s = pl.s;
+    it.h = pl.h;
     it.q_beg = q0;
     it.Lq = q1 - q0;
     it.k_beg = k0;
@@ -427,6 +446,10 @@ static void launch_t(const Args& a0, int max_q, int n_cu, hipStream_t st) {
   Args a = a0;
   constexpr int BQ = 32 * (kWaves / (G / 2));
   a.n_qblocks = (int)cdiv(max_q, BQ);
+  // segments per item chunk: K/V rows of a chunk's segments for one head
+  // about 2 MiB (half an XCD's L2), at least one segment
+  const int64_t kv_head_bytes = (int64_t)std::max(a.max_k, 1) * D * 2 * 2;
+  a.chunk_segs = (int)std::max<int64_t>(1, std::min<int64_t>(a.n_seqs, (int64_t(2) << 20) / kv_head_bytes));
   const int64_t n_items = (int64_t)a.hkv * a.n_seqs * a.n_qblocks;
   const int grid = (int)std::min<int64_t>(n_items, n_cu);
   hipLaunchKernelGGL((prefill_wide_kernel<G, CAUSAL, STORE, F16>), dim3(grid), dim3(kThreads), 0, st, a);
