@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/aac_attn.h"
 
 namespace aac {
@@ -141,5 +143,30 @@ __device__ __forceinline__ float vmax(float a, float b) { return __builtin_eleme
 __device__ __forceinline__ float vmax3(float a, float b, float c) { return vmax(vmax(a, b), c); }
 
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------- host
+// Compute units of the current device (the persistent grid size), cached per
+// device; a racing first query stores the same value twice.
+inline int device_cu_count(int* n_cu) {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *n_cu = c;
+      return AAC_OK;
+    }
+  }
+  int n = 0;
+  e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return (int)e;
+  if (n <= 0) return AAC_ERR_UNSUPPORTED;
+  if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  *n_cu = n;
+  return AAC_OK;
+}
+
 
 }  // namespace aac

@@ -707,29 +707,6 @@ static SplitPlan plan_split(int32_t n_seqs, int32_t max_q, int32_t max_k, int32_
   return p;
 }
 
-// Compute units of the current device (the persistent grid size), cached per
-// device; a racing first query stores the same value twice.
-static int device_cu_count(int* n_cu) {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return (int)e;
-  if (dev >= 0 && dev < 64) {
-    const int c = cache[dev].load(std::memory_order_relaxed);
-    if (c > 0) {
-      *n_cu = c;
-      return AAC_OK;
-    }
-  }
-  int n = 0;
-  e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e != hipSuccess) return (int)e;
-  if (n <= 0) return AAC_ERR_UNSUPPORTED;
-  if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
-  *n_cu = n;
-  return AAC_OK;
-}
-
 }  // namespace pf
 
 static int prefill_common(const void* q, const void* k, const void* v, int64_t q_tok_stride,
@@ -794,7 +771,7 @@ static int prefill_common(const void* q, const void* k, const void* v, int64_t q
   a.ws_cnt = nullptr;
   const bool f16 = dtype == AAC_DTYPE_FP16;
   int n_cu = 0;
-  int rc = pf::device_cu_count(&n_cu);
+  int rc = device_cu_count(&n_cu);
   if (rc != AAC_OK) return rc;
   // split keys when a workspace is given, the plan asks for it and the
   // workspace holds it (otherwise the call runs unsplit)
@@ -838,7 +815,7 @@ extern "C" size_t aac_prefill_workspace_bytes(int32_t n_seqs, int32_t max_seqlen
                                               int32_t causal) {
   if (head_dim != pf::D) return 0;
   int n_cu = 0;
-  if (pf::device_cu_count(&n_cu) != AAC_OK) return 0;
+  if (device_cu_count(&n_cu) != AAC_OK) return 0;
   return pf::plan_split(n_seqs, max_seqlen_q, max_seqlen_k, n_q_heads, n_kv_heads, causal != 0, n_cu)
       .ws_bytes;
 }
