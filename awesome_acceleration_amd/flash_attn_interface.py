@@ -119,11 +119,28 @@ def _prefill_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     with _ws_lock:
         buf = _pf_ws.get(key)
         if buf is None or buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                # under graph capture the fill would be recorded, not run, so
+                # the counters of a new buffer would not start at zero: the
+                # call runs unsplit instead
+                return None
             if buf is not None:
                 _ws_retired.append(buf)
             buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             _pf_ws[key] = buf
         return buf
+
+
+_PF_COUNTER_BYTES = 16 << 10  # the split prefill's per-item counters at the workspace start
+
+
+def _check_prefill_counters(ws: torch.Tensor) -> None:
+    """With ``AAC_CHECK``: the split prefill leaves its per-item counters at
+    zero; anything else means a workspace that was not zero-filled or was
+    shared by overlapping calls, and rows may have been left unwritten."""
+    if int(ws[:_PF_COUNTER_BYTES].count_nonzero()):
+        raise RuntimeError("split-prefill workspace counters are not zero after the call: the "
+                           "workspace was not zero-filled or is shared by overlapping calls")
 
 
 # ---------------------------------------------------------------- KV store
@@ -235,9 +252,11 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
         q.data_ptr(), k.data_ptr(), v.data_ptr(), qs, ks, vs, cu_seqlens_q.data_ptr(),
         cu_seqlens_k.data_ptr(), n_seqs, int(max_seqlen_q), int(max_seqlen_k),
         q.shape[1], k.shape[1], q.shape[2], scale, int(bool(causal)), out.data_ptr(),
-        out.stride(0), ws.data_ptr() if ws is not None else None, ws_bytes, _dtype_code(q),
-        _stream(q))
+        out.stride(0), ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0, _dtype_code(q), _stream(q))
     _lib.check(rc, "aac_prefill_varlen")
+    if _CHECK and ws is not None:
+        _check_prefill_counters(ws)
     return out
 
 

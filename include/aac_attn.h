@@ -220,8 +220,8 @@ int aac_decode_paged(const void* q, int64_t q_seq_stride, const void* k_cache, c
  * that overlap on one GPU -- other streams or threads -- race and must be
  * serialised by the caller; each call writes every scratch slot it reads, so
  * nothing carries over between calls.
- * No counterpart in the reference (whose flash_attn_with_kvcache allocates
- * its split buffers itself): an extra for callers that cannot allocate.
+ * No counterpart in the reference: an extra for callers that cannot
+ * allocate.
  */
 int aac_decode_paged_noalloc(const void* q, int64_t q_seq_stride, const void* k_cache,
                              const void* v_cache, int64_t num_blocks, int32_t block_size,

@@ -277,6 +277,7 @@ def _unsplit(q, k, v, cq, ck, Lq, Lk, causal, scale):
     ([512], [2048], 32, 8, False, torch.bfloat16),          # non-causal, Lq != Lk
     ([1500], [1500], 8, 8, True, torch.float16),
     ([200, 5, 600], [260, 5, 1200], 16, 4, True, torch.bfloat16),  # Lq < Lk, bottom-right
+    ([4096], [4096], 8, 1, True, torch.bfloat16),          # group 8: one 32-query slot, 8 heads
 ])
 def test_split_keys_match_unsplit_and_oracle(gpu, lens_q, lens_k, hq, hkv, causal, dtype):
     """Few work items: the key range of every item is split over several

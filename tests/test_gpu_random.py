@@ -206,7 +206,7 @@ def test_prefill_split_random(gpu, seed):
     second call and both it and the unsplit kernel meet the parity bound."""
     rs = np.random.RandomState(7000 + seed)
     hkv = int(rs.choice([1, 2, 4, 8]))
-    hq = hkv * int(rs.choice([1, 2, 4]))
+    hq = hkv * int(rs.choice([1, 2, 4, 8]))
     nseg = int(rs.randint(1, 4))
     lq = [int(x) for x in rs.randint(700, 4200, nseg)]
     if nseg > 1 and rs.randint(3) == 0:

@@ -96,3 +96,51 @@ def test_noalloc_refuses_a_plan_beyond_the_scratch(gpu):
     rc = L.aac_decode_paged_noalloc(p, 4096, p, p, 1 << 16, 256, p, 256, p, 1024, 0, 32, 8, 128,
                                     0.088, p, 4096, 256, 0, None)
     assert rc == -6 and b"scratch" in L.aac_strerror(rc)
+
+
+_CAPTURE_CHILD = r"""
+import sys
+import torch
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+from awesome_acceleration_amd import flash_attn_interface as fai
+import test_zz_no_alloc as t
+
+gpu = torch.device("cuda:0")
+x = t._case(gpu, 16, 32, 8, 16384, 24577, 21)
+
+def eager():
+    return fai.decode_paged(x["q"], x["kc"], x["vc"], x["bt_g"], x["ctx_g"],
+                            max_context_len=x["max_ctx"])
+
+ref = eager()
+out = torch.full_like(x["q"], float("nan"))
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):  # the process's first aac_decode_paged_noalloc call
+    t._noalloc(x, out)
+torch.cuda.synchronize()
+for i in range(3):
+    out.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+    again = eager()  # eager work between the replays
+    torch.cuda.synchronize()
+    assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
+print("capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture(gpu):
+    """A fresh process whose first no-alloc call is made under HIP graph
+    capture (the scratch address is looked up then): the captured graph,
+    replayed three times with eager calls in between, gives the eager
+    workspace entry point's result bit for bit."""
+    import os
+    import subprocess
+    import sys
+    print("case: decode_paged_noalloc first called under graph capture (child process)", flush=True)
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD, root, here], capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0 and "capture ok" in r.stdout, (r.stdout[-2000:], r.stderr[-4000:])
