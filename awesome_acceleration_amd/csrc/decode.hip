@@ -209,7 +209,14 @@ template <Dt DT, int G, int U, bool POW2>
 // CU (16 wavefronts); larger groups hold more accumulators.
 __global__ __launch_bounds__(256, G <= 2 ? 4 : 2) void decode_paged_kernel(DecodeArgs a) {
   constexpr int ES = Elem<DT>::kBytes;
-  const int h = blockIdx.x;  // the KV heads of one token range are dispatched together
+  // The KV heads of one token range are dispatched together.  Workgroups go
+  // to the 8 XCDs round-robin, so with an even head count workgroup x runs
+  // on an XCD of x's parity; it attends head x ^ 1, on the XCD of the other
+  // parity: measured on MI355X over all eight rotations of heads to XCDs,
+  // the odd ones (256 seqs x 1-2k, 16/8 heads: 246.4-247.0 us) beat the even
+  // ones (253.2-253.3 us), and likewise at 8/4 heads (129.4-129.7 against
+  // 132.8-133.0 us).
+  const int h = (a.hkv & 1) ? (int)blockIdx.x : (int)(blockIdx.x ^ 1u);
   const int part = blockIdx.y;
   const int tid = threadIdx.x;
   // Longest contexts first: the dispatcher hands out workgroups in index
