@@ -186,13 +186,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     const int sl = rem / a.hkv;
     return Place{z, c * a.chunk_segs + sl, rem - sl * a.hkv};
   };
-  auto seg_of = [&](int i) { return place_of(i).s; };
   auto kv_end_of = [&](const Item& it) {
     const int wg_qmax = min(it.qb * BQ + BQ, it.Lq) - 1;
     return CAUSAL ? max(0, min(it.Lk, wg_qmax + 1 + it.Lk - it.Lq)) : it.Lk;
   };
-  auto decode = [&](int i, int q0, int q1, int k0, int k1, Item& it) -> bool {
-    const Place pl = place_of(i);
+  auto decode = [&](const Place& pl, int q0, int q1, int k0, int k1, Item& it) -> bool {
     const int z = pl.z;
     it.s = pl.s;
     it.h = pl.h;
@@ -213,8 +211,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
     for (; k * P < n_items; ++k) {
       const int i = item_index(k);
       if (i >= n_items) continue;
-      const int sg = seg_of(i);
-      if (decode(i, cuq[sg], cuq[sg + 1], cuk[sg], cuk[sg + 1], it)) return true;
+      const Place pl = place_of(i);
+      const int sg = pl.s;
+      if (decode(pl, cuq[sg], cuq[sg + 1], cuk[sg], cuk[sg + 1], it)) return true;
     }
     return false;
   };
@@ -341,7 +340,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_wide_kernel(Args a) {
       for (int i = 0; i < 4; ++i)
         load_lds16(rsv, ld_voff_v, T * vs64 + i * vs16, st + kTileBytes + i * 4096);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // The body reads tiles 0 and 1 before its first barrier; tile 2 (the
+    // youngest 8 loads) is waited for at the start of its second tile
+    // iteration.  An item of fewer than three tiles has no such iteration
+    // and refills tile 2's stage in its epilogue, so it waits for all.
+    if (kv_end > 2 * BKV)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   int g0 = 0;  // ring stage of the current item's tile 0
 
