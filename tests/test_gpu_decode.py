@@ -136,6 +136,27 @@ def test_decode_256_seqs_full_size(gpu):
                     what="decode 256 seqs", absv=np.stack([absv[b] for b in range(B)]))
 
 
+@pytest.mark.parametrize("hq,hkv", [(6, 3), (12, 3), (10, 5), (16, 2)])
+def test_decode_kv_head_counts_odd_and_even(gpu, hq, hkv):
+    # The grid's workgroup x attends KV head x ^ 1 when the head count is
+    # even (the head's XCD is then of the other parity) and head x when it is
+    # odd: every head of every sequence must still be attended exactly once.
+    print(f"case: decode {hq}/{hkv} heads", flush=True)
+    B, bs = 24, 64
+    rs = np.random.RandomState(hq * 16 + hkv)
+    ctx = rs.randint(1, 700, B).astype(np.int32)
+    q, kc, vc, kn, vn, bt = _random_paged(B, hq, hkv, ctx, bs, 7, gpu)
+    scale = 128 ** -0.5
+    out = fai.decode_paged(q, kc, vc, torch.from_numpy(bt).to(gpu), torch.from_numpy(ctx).to(gpu),
+                           scale)
+    torch.cuda.synchronize()
+    kc_np, vc_np, q_np = np_of(kc), np_of(vc), np_of(q)
+    ref = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), scale)
+    absv = _oracle_rows(kc_np, vc_np, q_np, bt, ctx, bs, range(B), scale, abs_v=True)
+    check_attention(out, np.stack([ref[b] for b in range(B)]), what=f"decode {hq}/{hkv}",
+                    absv=np.stack([absv[b] for b in range(B)]))
+
+
 def test_decode_long_context_gqa4_sampled(gpu):
     # bf16, B=64, 32 query / 8 KV heads, context ~ U[16384, 32768]: split-K
     # with the log-sum-exp reduction.  8 sequences are checked against the
