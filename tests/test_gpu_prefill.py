@@ -217,7 +217,11 @@ def test_empty_sequences_and_understated_max_seqlen_k(gpu):
 
 @pytest.mark.parametrize("hq,hkv,dtype", [(8, 8, torch.bfloat16), (16, 8, torch.bfloat16),
                                            (32, 8, torch.bfloat16), (64, 8, torch.bfloat16),
-                                           (16, 8, torch.float16), (64, 8, torch.float16)])
+                                           (16, 8, torch.float16), (64, 8, torch.float16),
+                                           # odd KV head counts (each kernel, each group)
+                                           (6, 3, torch.bfloat16), (12, 3, torch.bfloat16),
+                                           (24, 3, torch.bfloat16), (5, 5, torch.bfloat16),
+                                           (10, 5, torch.float16)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_store_in_the_attention_kernel_covers_every_token(gpu, hq, hkv, dtype, causal):
     # One cu_seqlens array for queries and keys: the store runs inside the
