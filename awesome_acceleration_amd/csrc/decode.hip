@@ -532,7 +532,13 @@ static DecodePlan plan_decode(int32_t n_seqs, int32_t hq, int32_t hkv, int32_t b
 
 template <Dt DT, int G>
 static void launch_decode_t(const DecodeArgs& a, hipStream_t s) {
-  constexpr int U = G >= 8 ? 4 : 8;  // token rows in flight per DPP row
+  // Token rows in flight per DPP row: eight for bf16/fp16, four for fp32,
+  // whose rows take twice the registers (at eight, the fp32 instances of
+  // groups 1 and 2 spill under the 128-VGPR bound of four workgroups per
+  // CU).  At bf16 group 8, eight rows (233 VGPRs, 2 workgroups per CU) beat
+  // four (181) by 3% on 256 seqs x 1-2k at 64/8 heads (318.0 against
+  // 328.2 us).
+  constexpr int U = DT == Dt::FP32 ? 4 : 8;
   dim3 grid(a.hkv, a.n_parts, a.n_seqs);
   if (a.bs_shift >= 0)
     hipLaunchKernelGGL((decode_paged_kernel<DT, G, U, true>), grid, dim3(256), 0, s, a);
