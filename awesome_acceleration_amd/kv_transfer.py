@@ -35,7 +35,11 @@ def _check_storage(storage: torch.Tensor) -> None:
     _require(storage.is_cuda, "the KV cache must be on a GPU (no CPU path exists)")
     _require(storage.dim() == 6 and storage.shape[1] == 2,
              "KV storage must be [n_layers, 2, num_blocks, block_size, Hkv, D]")
-    _require(storage.is_contiguous(), "KV storage must be contiguous")
+    _, _, nb, bs, hkv, d = storage.shape
+    _require(storage.stride()[2:] == (bs * hkv * d, hkv * d, d, 1),
+             "each layer's K and V cache in the KV storage must be contiguous")
+    _require(storage.stride(1) >= nb * bs * hkv * d and storage.stride(0) >= 2 * storage.stride(1),
+             "the KV storage's layer and K/V strides must not overlap its caches")
 
 
 def _table(block_table, device) -> torch.Tensor:

@@ -34,6 +34,7 @@ import torch.nn.functional as F
 from . import flash_attn_interface as fai
 from . import fused as fz
 from . import kv_transfer
+from . import paged
 
 __all__ = ["Qwen3Config", "Qwen3ForCausalLM", "PagedKVCache", "StepMeta"]
 
@@ -96,14 +97,16 @@ class Rope:
 
 class PagedKVCache:
     """Per-layer paged K/V caches ``[num_blocks, block_size, Hkv, D]``,
-    zero-initialised like model/model.py:328-335."""
+    zero-initialised like model/model.py:328-335, in one strided storage
+    ``[n_layers, 2, ...]`` whose V caches sit 512 bytes (modulo 1 KiB) from
+    their K caches (``paged.alloc_kv_storage``)."""
 
     def __init__(self, cfg: Qwen3Config, num_blocks: int, block_size: int, device, dtype):
         self.num_blocks = num_blocks
         self.block_size = block_size
-        shape = (cfg.num_hidden_layers, 2, num_blocks, block_size, cfg.num_key_value_heads,
-                 cfg.head_dim)
-        self.storage = torch.zeros(shape, device=device, dtype=dtype)
+        self.storage = paged.alloc_kv_storage(cfg.num_hidden_layers, num_blocks, block_size,
+                                              cfg.num_key_value_heads, cfg.head_dim,
+                                              dtype=dtype, device=device)
 
     def k(self, layer: int) -> torch.Tensor:
         return self.storage[layer, 0]
@@ -113,7 +116,7 @@ class PagedKVCache:
 
     @property
     def nbytes(self) -> int:
-        return self.storage.numel() * self.storage.element_size()
+        return self.storage.untyped_storage().nbytes()
 
     def export_request_kv(self, block_table, length: int, seqlen: int) -> dict:
         """The reference's export_request_kv (model/model.py:386-390) for the

@@ -80,6 +80,8 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_PROFILE = "profiles/decode_256seq_ctx1k-2k_bf16_traffic.md"
+CACHE_LAYOUT_NOTE = ("K/V caches placed as the engine's PagedKVCache places them "
+                     "(paged.alloc_kv_cache: V 512 B past K modulo 1 KiB)")
 TRAFFIC_PREFILL = "profiles/prefill_8x1024_bf16_traffic.md"
 TRAFFIC_PREFILL_LONG = "profiles/prefill_8x8192_bf16_traffic.md"
 TRAFFIC_PREFILL_ENGINE = "profiles/prefill_engine_256x1024_bf16_traffic.md"
@@ -139,7 +141,11 @@ def parse():
 # decode: 256 seqs x ctx U[1024, 2047]
 # ----------------------------------------------------------------------------
 def make_decode_inputs(torch, dev, seed, B=256, hq=16, hkv=8, d=128, bs=256, ctx_lo=1024,
-                       ctx_hi=2048):
+                       ctx_hi=2048, layout="engine"):
+    """Synthetic decode inputs.  layout "engine": the K/V caches placed as the
+    engine's cache places them (paged.alloc_kv_cache: the V cache 512 bytes
+    past its K cache modulo 1 KiB); "separate": two separate allocations, as
+    the reference's two torch.zeros (model/model.py:328-335)."""
     rs = np.random.RandomState(seed)
     ctx = rs.randint(ctx_lo, ctx_hi, B).astype(np.int32)      # after the store
     need = [int(-(-c // bs)) for c in ctx]
@@ -153,12 +159,19 @@ def make_decode_inputs(torch, dev, seed, B=256, hq=16, hkv=8, d=128, bs=256, ctx
         k0 += n
     g = torch.Generator(device=dev).manual_seed(seed)
     bf = torch.bfloat16
-    kc = torch.randn((pool, bs, hkv, d), generator=g, device=dev).to(bf)
-    vc = torch.randn((pool, bs, hkv, d), generator=g, device=dev).to(bf)
+    if layout == "engine":
+        from awesome_acceleration_amd import paged
+        kc, vc = paged.alloc_kv_cache(pool, bs, hkv, d, dtype=bf, device=dev)
+        kc.copy_(torch.randn((pool, bs, hkv, d), generator=g, device=dev))
+        vc.copy_(torch.randn((pool, bs, hkv, d), generator=g, device=dev))
+    else:
+        kc = torch.randn((pool, bs, hkv, d), generator=g, device=dev).to(bf)
+        vc = torch.randn((pool, bs, hkv, d), generator=g, device=dev).to(bf)
     q = torch.randn((B, 1, hq, d), generator=g, device=dev).to(bf)
     kn = torch.randn((B, 1, hkv, d), generator=g, device=dev).to(bf)
     vn = torch.randn((B, 1, hkv, d), generator=g, device=dev).to(bf)
     return dict(ctx=ctx, bt=bt, kc=kc, vc=vc, q=q, kn=kn, vn=vn, B=B, hq=hq, hkv=hkv, d=d, bs=bs,
+                v_minus_k_mod_1k=(vc.data_ptr() - kc.data_ptr()) % 1024,
                 bt_g=torch.from_numpy(bt).to(dev),
                 seqlens_g=torch.from_numpy(ctx - 1).to(dev),
                 ctx_g=torch.from_numpy(ctx).to(dev))
@@ -228,9 +241,30 @@ def bench_decode(torch, fai, dev, args, hq=16, hkv=8):
     # the attention launch alone, HIP events on the launch stream
     t_att = launch_avg(torch, attend, args.steps)
     achieved = attend_bytes / t_att / 1e9
+    t_sep = separate_caches_time(torch, fai, x, maxctx, args)
     return dict(
         t_step=t_step, step_bytes=step_bytes, attend_bytes=attend_bytes, t_attend=t_att,
-        achieved=achieved, x=x)
+        achieved=achieved, x=x, t_attend_separate=t_sep)
+
+
+def separate_caches_time(torch, fai, x, maxctx, args):
+    """The same attention over copies of the caches in two separate
+    allocations (the reference's placement), for comparison: HIP-event time
+    per launch and the V cache's offset from the K cache modulo 1 KiB."""
+    kc, vc = x["kc"].clone(), x["vc"].clone()
+    q3 = x["q"].view(x["B"], x["hq"], x["d"])
+    out3 = torch.empty_like(q3)
+
+    def attend():
+        return fai.decode_paged(q3, kc, vc, x["bt_g"], x["ctx_g"], max_context_len=maxctx,
+                                partition_tokens=getattr(args, "partition", 0), out=out3)
+
+    warm(torch, [attend], min(args.warmup_seconds, 0.5))
+    t = launch_avg(torch, attend, args.steps)
+    off = (vc.data_ptr() - kc.data_ptr()) % 1024
+    del kc, vc
+    torch.cuda.empty_cache()
+    return t, off
 
 
 # ----------------------------------------------------------------------------
@@ -279,7 +313,8 @@ def bench_decode_fp32_small(torch, fai, dev, args):
 # [slots, max_seq_len, Hkv, D] picked by cache_batch_idx (model/model.py:233-240)
 # ----------------------------------------------------------------------------
 def bench_decode_slot(torch, fai, dev, args, lmax=2064):
-    x = make_decode_inputs(torch, dev, args.seed, bs=lmax)  # one block (slot) per sequence
+    # one block (slot) per sequence; the caches allocated apart, as the reference allocates them
+    x = make_decode_inputs(torch, dev, args.seed, bs=lmax, layout="separate")
     attend_bytes, step_bytes = decode_bytes(x)
     slots = x["bt_g"][:, 0].contiguous()
 
@@ -323,11 +358,15 @@ def bench_decode_long(torch, fai, dev, args):
     warm(torch, [attend], args.warmup_seconds)
     t = launch_avg(torch, attend, args.steps)
     ach = attend_bytes / t / 1e9
+    t_sep, off = separate_caches_time(torch, fai, x, maxctx, args)
     return {
         "workload": "paged decode attend, 64 seqs, 32 q / 8 kv heads (GQA-4), head_dim 128, "
                     "context U[16384,32768], block 256, split-K with log-sum-exp reduction (auto plan)",
         "context_tokens": int(x["ctx"].sum()),
+        "cache_layout": CACHE_LAYOUT_NOTE,
         "us_per_call": round(t * 1e6, 2),
+        "separate_caches": {"us_per_call": round(t_sep * 1e6, 2), "v_minus_k_mod_1k": off,
+                            "frac": round(attend_bytes / t_sep / 1e9 / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "bytes_per_call": attend_bytes,
                      "traffic": measured_traffic(TRAFFIC_DECODE_LONG),
@@ -908,7 +947,13 @@ def main():
             "decode": {"us_per_launch": round(dec2["t_attend"] * 1e6, 2),
                        "achieved": round(dec2["achieved"], 2), "unit": "GB/s",
                        "frac": round(dec2["achieved"] / HBM_PEAK_GBS, 4),
-                       "bytes_per_launch": dec2["attend_bytes"]},
+                       "bytes_per_launch": dec2["attend_bytes"],
+                       "cache_layout": CACHE_LAYOUT_NOTE,
+                       "separate_caches": {
+                           "us_per_launch": round(dec2["t_attend_separate"][0] * 1e6, 2),
+                           "v_minus_k_mod_1k": dec2["t_attend_separate"][1],
+                           "frac": round(dec2["attend_bytes"] / dec2["t_attend_separate"][0] / 1e9
+                                         / HBM_PEAK_GBS, 4)}},
             "prefill": {"us_attend": round(pf2["t_attend"] * 1e6, 2),
                         "achieved": round(pf2["tflops"], 2), "unit": "TFLOP/s",
                         "frac": round(pf2["tflops"] / BF16_PEAK_TFLOPS, 4),
@@ -955,7 +1000,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) q/k/v and caches, random shuffled block tables)",
+        "data": "synthetic (seeded N(0,1) q/k/v and caches, random shuffled block tables; the paged "
+                "K/V caches placed as the engine places them, separately allocated caches timed beside)",
         "device": device_record(torch, dev),
         "config": {
             "workload": "paged decode store+attend, 256 seqs, 16 q / 8 kv heads, head_dim 128, "
@@ -975,6 +1021,12 @@ def main():
             "traffic_source": TRAFFIC_PROFILE,
             "bytes_per_launch": dec["attend_bytes"],
             "us_per_launch": round(dec["t_attend"] * 1e6, 2),
+            "cache_layout": CACHE_LAYOUT_NOTE,
+            "separate_caches": {
+                "us_per_launch": round(dec["t_attend_separate"][0] * 1e6, 2),
+                "v_minus_k_mod_1k": dec["t_attend_separate"][1],
+                "frac": round(dec["attend_bytes"] / dec["t_attend_separate"][0] / 1e9 / HBM_PEAK_GBS, 4),
+            },
         },
     }
     if "prefill" in res:

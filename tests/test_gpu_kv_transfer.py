@@ -73,4 +73,31 @@ def test_export_rejects_bad_shapes(gpu):
     with pytest.raises(RuntimeError):
         kt.kv_export(st, [0, 1], 40)  # 2 blocks of 16 cannot hold 40 tokens
     with pytest.raises(RuntimeError):
-        kt.kv_export(st[:, :, :2], [0], 8)  # not contiguous
+        kt.kv_export(st[..., ::2], [0], 8)  # a cache whose rows are not contiguous
+    # the first two blocks of every cache: strided, each cache contiguous; exports
+    # the same rows as a contiguous copy of them
+    part = st[:, :, :2]
+    got = kt.kv_export(part, [1, 0], 20)
+    torch.cuda.synchronize()
+    assert torch.equal(got, kt.kv_export(part.contiguous(), [1, 0], 20))
+
+
+def test_export_import_on_the_engine_cache_placement(gpu):
+    """The engine's storage (each layer's V cache 512 bytes past its K cache,
+    modulo 1 KiB) exports and imports like a contiguous one."""
+    print("case: kv export/import, engine cache placement", flush=True)
+    from awesome_acceleration_amd import paged
+    L, nb, bs, hkv, d, length = 3, 24, 32, 8, 128, 300
+    st = paged.alloc_kv_storage(L, nb, bs, hkv, d, dtype=torch.bfloat16, device=gpu)
+    st.copy_(_storage(L, nb, bs, hkv, d, torch.bfloat16, gpu, 5))
+    rs = np.random.RandomState(9)
+    bt = rs.permutation(nb)[:10].astype(np.int32)  # 10 blocks of 32 hold 300 tokens
+    out = kt.kv_export(st, torch.from_numpy(bt).to(gpu), length)
+    torch.cuda.synchronize()
+    assert np.array_equal(np_of(out), oracle.kv_export(np_of(st), bt, length))
+    dst = paged.alloc_kv_storage(L, nb, bs, hkv, d, dtype=torch.bfloat16, device=gpu)
+    dst.fill_(2.0)
+    kt.kv_import(out, dst, torch.from_numpy(bt).to(gpu), length)
+    torch.cuda.synchronize()
+    want = oracle.kv_import(np_of(out), np_of(torch.full_like(st, 2.0)), bt, length)
+    assert np.array_equal(np_of(dst), want)

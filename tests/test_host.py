@@ -168,3 +168,27 @@ def test_engine_rejects_a_request_larger_than_the_block_pool():
         llm.generate([[1] * 200], max_tokens=100)  # 300 tokens -> 5 blocks of 64
     llm.generate([[1] * 200], max_tokens=56)  # 256 tokens -> 4 blocks: accepted
     assert llm._request_queue.qsize() == 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("nb,bs,hkv", [(3, 16, 8), (5, 256, 4), (7, 100, 1)])
+def test_kv_storage_places_v_512_bytes_past_k(dtype, nb, bs, hkv):
+    L, d = 3, 128
+    st = paged.alloc_kv_storage(L, nb, bs, hkv, d, dtype=dtype, device="cpu")
+    es = st.element_size()
+    assert tuple(st.shape) == (L, 2, nb, bs, hkv, d) and st.dtype == dtype
+    assert not st.any()
+    part = nb * bs * hkv * d
+    for layer in range(L):
+        k, v = st[layer, 0], st[layer, 1]
+        assert k.is_contiguous() and v.is_contiguous()
+        gap = (v.data_ptr() - k.data_ptr())
+        assert gap % 1024 == paged.KV_SKEW_BYTES and gap >= part * es  # no overlap
+        if layer + 1 < L:
+            assert st[layer + 1, 0].data_ptr() - v.data_ptr() >= part * es
+    # the caches are distinct memory: writing one leaves every other untouched
+    st[1, 0].fill_(1)
+    assert int(st[1, 0].count_nonzero()) == part and int(st.count_nonzero()) == part
+    k, v = paged.alloc_kv_cache(nb, bs, hkv, d, dtype=dtype, device="cpu")
+    assert tuple(k.shape) == (nb, bs, hkv, d) and tuple(v.shape) == (nb, bs, hkv, d)
+    assert (v.data_ptr() - k.data_ptr()) % 1024 == paged.KV_SKEW_BYTES
