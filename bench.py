@@ -379,9 +379,10 @@ def bench_decode_long(torch, fai, dev, args):
 # 2048 tokens in 8 blocks of 256 drawn from a 2304-block pool
 # ----------------------------------------------------------------------------
 def bench_kv_transfer(torch, dev, args):
-    from awesome_acceleration_amd import kv_transfer as kt
+    from awesome_acceleration_amd import kv_transfer as kt, paged
     L, nb, bs, hkv, d, length = 28, 2304, 256, 8, 128, 2048
-    st = torch.empty((L, 2, nb, bs, hkv, d), dtype=torch.bfloat16, device=dev)
+    # the engine's cache storage (PagedKVCache): each layer's V cache 512 bytes from its K cache
+    st = paged.alloc_kv_storage(L, nb, bs, hkv, d, dtype=torch.bfloat16, device=dev)
     st.view(torch.int16).random_(-30000, 30000, generator=torch.Generator(device=dev).manual_seed(args.seed))
     bt = torch.randperm(nb, device=dev, generator=torch.Generator(device=dev).manual_seed(args.seed))
     bt = bt[:length // bs].to(torch.int32)
